@@ -1,0 +1,247 @@
+#!/usr/bin/env python3
+"""Benchmark of the quantized-linear hot path on one MI355X.
+
+Metric: "GPTQ-int4 decode matvec GB/s (% HBM peak) + prefill
+GEMM TFLOP/s (% MFMA)".
+
+A step is one batch-1 decode token through the Llama-7B-shaped GPTQ int4
+linears of BASELINE.json configs[1] (group 128, f32 activations):
+  q_proj   4096 x 4096                      st_gptq_i4_matvec
+  gate/up  4096 x (2 x 11008), silu(g) * u  st_gptq_i4_gate_up_silu
+  down     11008 x 4096, silu(a) * b input  st_gptq_i4_silu_matvec
+`value` = algorithmic bytes of the step / step time (GB/s), inputs resident
+in HBM. Cold cache: the weights are replicated `--copies` times (default:
+enough for > 512 MB, twice the MALL) and step i uses copy i % copies.
+
+Also reported: per-kernel HIP-event timings, the roofline of the dominant
+kernel (gate/up), the prefill GEMM when built, and the CPU
+baseline (the oracle's WGSL-order gptq_matvec_4t restatement on the host
+cores; the reference WGSL cannot run here: no wgpu/lavapipe).
+
+Usage: python bench.py [--gpus 1] [--steps 200] [--warmup 20]
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+METRIC = "GPTQ-int4 decode matvec GB/s (% HBM peak) + prefill GEMM TFLOP/s (% MFMA)"
+HBM_PEAK_GBS = 8000.0
+F16_MFMA_PEAK_TFLOPS = 2500.0
+GS = 128
+
+
+def decode_bytes(K, N, x_bytes, y_n, n_inputs=1):
+    """qweight K*N/2 + f16 scales 2*(K/g)*N + activations + f32 outputs."""
+    return K * N // 2 + 2 * (K // GS) * N + n_inputs * K * x_bytes + 4 * y_n
+
+
+def make_gptq(torch, dev, K, N, gen):
+    qw = torch.randint(-(2**31), 2**31 - 1, (K // 8, N), dtype=torch.int32, device=dev, generator=gen)
+    sc = (torch.randn(K // GS, N, device=dev, generator=gen) * 0.02).abs().half()
+    return qw, sc
+
+
+def time_loop(torch, fn, iters, warmup):
+    for i in range(warmup):
+        fn(i)
+    s = torch.cuda.current_stream()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    e0.record(s)
+    for i in range(iters):
+        fn(i)
+    e1.record(s)
+    torch.cuda.synchronize()
+    return e0.elapsed_time(e1) / iters  # ms
+
+
+def cpu_baseline(seconds=10.0):
+    """Oracle restatement of gptq_matvec_4t (src/shaders/gptq_matvec_4t.wgsl)
+    on the host cores, q_proj shape (4096 x 4096, f32 x), repeated for about
+    `seconds`. Reported beside the GPU figure; not the optimisation target."""
+    import numpy as np
+
+    import oracle as O
+
+    K = N = 4096
+    c = O.gptq_case(0, K, N, GS)
+    try:
+        cores = len(os.sched_getaffinity(0))
+    except AttributeError:
+        cores = os.cpu_count() or 1
+    cores = max(1, min(cores, 16))
+    _, used = O.gptq_matvec_4t_omp(c["x"], c["qweight"], c["scales"], K, N, GS, cores)
+    reps, t0 = 0, time.perf_counter()
+    while True:
+        O.gptq_matvec_4t_omp(c["x"], c["qweight"], c["scales"], K, N, GS, cores)
+        reps += 1
+        el = time.perf_counter() - t0
+        if el >= seconds:
+            break
+    per = el / reps
+    b = decode_bytes(K, N, 4, N)
+    return {"value": round(b / per / 1e9, 3), "unit": "GB/s", "cores": int(used), "kind": "port",
+            "sample": f"oracle gptq_matvec_4t restatement (WGSL order, OpenMP over columns), q_proj 4096x4096 "
+                      f"f32 x, {reps} calls in {el:.1f} s ({per * 1e3:.2f} ms/call)"}
+
+
+def load_traffic():
+    """HBM bytes per launch of the dominant kernel from committed rocprofv3
+    --pmc runs (profiles/gate_up_traffic.json), if measured."""
+    p = os.path.join(ROOT, "profiles", "gate_up_traffic.json")
+    if os.path.exists(p):
+        with open(p) as f:
+            return json.load(f).get("traffic_bytes_per_launch")
+    return None
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--copies", type=int, default=0, help="weight copies for cold-cache rotation (0 = auto)")
+    ap.add_argument("--cpu-seconds", type=float, default=10.0)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-gemm", action="store_true")
+    ap.add_argument("--only", default="", help="profile helper: run only this kernel (q|gate_up|down|gemm)")
+    args = ap.parse_args()
+    world = int(os.environ.get("WORLD_SIZE", "1"))
+    if args.gpus != 1 or world != 1:
+        print("bench.py: this build measures one GPU; multi-GPU runs are not part of it "
+              "(the decode matvec would shard column-parallel, see DESIGN.md)", file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+
+    import shady_thinker_amd as sta
+    from shady_thinker_amd import model as Mdl
+
+    dev = torch.device("cuda", 0)
+    torch.cuda.set_device(dev)
+    gpu = sta.GpuContext(0)
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(0)
+
+    H, I = 4096, 11008
+    shapes = {"q": (H, H), "gate_up": (H, I), "down": (I, H)}
+    b_q = decode_bytes(H, H, 4, H)
+    b_gu = decode_bytes(H, 2 * I, 4, I)  # two weights of 4096 x 11008, one f32 output per column pair
+    b_dn = decode_bytes(I, H, 4, H, n_inputs=2)  # a and b
+    step_bytes = b_q + b_gu + b_dn
+    copies = args.copies or max(2, -(-2 * 256 * 2**20 // step_bytes) + 1)
+
+    W = []
+    for _ in range(copies):
+        W.append({
+            "q": make_gptq(torch, dev, H, H, gen),
+            "g": make_gptq(torch, dev, H, I, gen),
+            "u": make_gptq(torch, dev, H, I, gen),
+            "d": make_gptq(torch, dev, I, H, gen),
+        })
+    x = torch.randn(1, H, device=dev, generator=gen)
+    yq = torch.empty(1, H, device=dev)
+    a = torch.randn(1, I, device=dev, generator=gen)
+    b = torch.randn(1, I, device=dev, generator=gen)
+    ygu = torch.empty(1, I, device=dev)
+    ydn = torch.empty(1, H, device=dev)
+
+    def k_q(i):
+        w = W[i % copies]["q"]
+        Mdl.gptq_matvec(gpu, "q_proj", x, w[0], w[1], yq, H, H, GS)
+
+    def k_gu(i):
+        w = W[i % copies]
+        Mdl.fused_gate_up_silu(gpu, x, w["g"][0], w["g"][1], w["u"][0], w["u"][1], ygu, H, I, GS)
+
+    def k_dn(i):
+        w = W[i % copies]["d"]
+        Mdl.fused_silu_gptq_down(gpu, a, b, w[0], w[1], ydn, I, H, GS)
+
+    def step(i):
+        k_q(i)
+        k_gu(i)
+        k_dn(i)
+
+    if args.only:
+        fn = {"q": k_q, "gate_up": k_gu, "down": k_dn}.get(args.only)
+        if fn is not None:
+            time_loop(torch, fn, args.steps, args.warmup)
+            print(json.dumps({"only": args.only, "steps": args.steps}))
+            return
+
+    ms_step = time_loop(torch, step, args.steps, args.warmup)
+    ms_q = time_loop(torch, k_q, args.steps, args.warmup)
+    ms_gu = time_loop(torch, k_gu, args.steps, args.warmup)
+    ms_dn = time_loop(torch, k_dn, args.steps, args.warmup)
+    value = step_bytes / (ms_step * 1e-3) / 1e9
+    gu_gbs = b_gu / (ms_gu * 1e-3) / 1e9
+
+    out = {
+        "metric": METRIC,
+        "value": round(value, 2),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_step, 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "int4xf32",
+        "data": "synthetic (torch RNG: uniform nibbles, |N(0,0.02)| f16 scales, N(0,1) f32 activations)",
+        "config": {
+            "workload": "configs[1]: Llama-7B decode linears, GPTQ int4 g128, batch 1: q_proj 4096x4096 + "
+                        "fused gate/up 4096x(2x11008) + fused silu down 11008x4096",
+            "batch": 1, "group_size": GS, "cold_cache_copies": copies,
+            "step_bytes": step_bytes, "hbm_frac": round(value / HBM_PEAK_GBS, 4),
+        },
+        "kernels": {
+            "q_proj": {"ms": round(ms_q, 5), "bytes": b_q, "GB/s": round(b_q / ms_q / 1e6, 1)},
+            "gate_up": {"ms": round(ms_gu, 5), "bytes": b_gu, "GB/s": round(gu_gbs, 1)},
+            "down": {"ms": round(ms_dn, 5), "bytes": b_dn, "GB/s": round(b_dn / ms_dn / 1e6, 1)},
+        },
+        "roofline": {"bound": "hbm", "kernel": "qmv_kernel gate/up (st_gptq_i4_gate_up_silu)",
+                     "achieved": round(gu_gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(gu_gbs / HBM_PEAK_GBS, 4), "traffic": load_traffic()},
+    }
+
+    if not args.no_gemm:
+        out["gemm"] = bench_gemm(torch, dev, gpu, Mdl, gen, args)
+
+    if not args.no_cpu_baseline:
+        out["cpu_baseline"] = cpu_baseline(args.cpu_seconds)
+    gpu.close()
+    print(json.dumps(out))
+
+
+def bench_gemm(torch, dev, gpu, Mdl, gen, args):
+    """int4 prefill GEMM with act-order, M = 2048, K = 4096,
+    N = 14336, f16 A, f16 C."""
+    import shady_thinker_amd as sta
+
+    Mr, K, N = 2048, 4096, 14336
+    qw, sc = make_gptq(torch, dev, K, N, gen)
+    perm = torch.randperm(K, device=dev, generator=gen).to(torch.int32)
+    A = torch.randn(Mr, K, device=dev, generator=gen).half()
+    C = torch.empty(Mr, N, device=dev, dtype=torch.float16)
+    try:
+        Mdl.gptq_gemm(gpu, A, qw, sc, C, K, N, GS, None, perm)
+    except sta.ShadyHipError as e:
+        return {"status": "not available", "error": str(e)}
+    iters = max(5, min(50, args.steps // 4))
+    ms = time_loop(torch, lambda i: Mdl.gptq_gemm(gpu, A, qw, sc, C, K, N, GS, None, perm), iters, 3)
+    tf = 2.0 * Mr * K * N / (ms * 1e-3) / 1e12
+    return {"M": Mr, "K": K, "N": N, "act_order": True, "ms": round(ms, 4), "TFLOP/s": round(tf, 1),
+            "mfma_frac": round(tf / F16_MFMA_PEAK_TFLOPS, 4), "peak_TFLOP/s": F16_MFMA_PEAK_TFLOPS}
+
+
+if __name__ == "__main__":
+    main()

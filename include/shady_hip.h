@@ -1,0 +1,186 @@
+/*
+ * shady_hip.h: C ABI of the MI355X (gfx950) quantized-linear backend.
+ *
+ * Drop-in for the GPTQ linear path of tmzt/shady-thinker: the Rust host keeps
+ * `Model::gptq_matvec` / `Model::fused_silu_gptq_down` and its call sites
+ * (src/model.rs:357-408, called from Model::forward src/model.rs:669-969 and
+ * InferenceSession::generate_tokens src/inference.rs:72-131); inside, those
+ * helpers call these functions instead of GpuContext::dispatch
+ * (src/gpu.rs:188-234) with a WGSL shader.
+ *
+ * Conventions
+ *  - Plain pointers and sizes only. Every tensor argument is a device pointer
+ *    (from st_alloc or any hipMalloc allocation) unless the name says `host`.
+ *  - Layouts are the reference's, unmodified (src/weights.rs:398 uploads the
+ *    GPTQ safetensors bytes verbatim):
+ *      qweight u32[K/8, N]  eight 4-bit values per word along K, low nibble =
+ *                           lowest k (src/shaders/gptq_matvec.wgsl:51-59)
+ *      scales  f16[K/gs, N] (read as u32 pairs by the WGSL, :41-45)
+ *      qzeros  u32[K/gs, N/8] eight zero points per word along N (AutoGPTQ;
+ *                           dropped by the reference, src/weights.rs:372-374)
+ *      x       [M, K] row-major, y [M, N] row-major (M = 1 for decode)
+ *    INT8 weights (no reference counterpart) are int8[N, K] row-major with
+ *    f32 per-output-channel scales[N].
+ *  - Every call is asynchronous and ordered on the context's stream, like the
+ *    reference's single queue (src/gpu.rs:176-242). st_flush() waits.
+ *  - Return value: ST_OK (0) or an st_status code; st_last_error() gives the
+ *    message for the calling thread. The Rust side `expect`s on non-zero to
+ *    keep the reference's panic semantics.
+ *  - A context is not thread-safe (the reference serialises through
+ *    `&mut GpuContext`).
+ */
+#ifndef SHADY_HIP_H
+#define SHADY_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef struct st_context st_context;
+
+typedef enum {
+    ST_OK = 0,
+    ST_ERR_INVALID = 1,     /* null pointer / bad enum */
+    ST_ERR_SHAPE = 2,       /* K, N, M or group size not supported */
+    ST_ERR_ALIGN = 3,       /* pointer not 16-byte aligned */
+    ST_ERR_UNSUPPORTED = 4, /* valid request this build does not implement */
+    ST_ERR_HIP = 5,         /* HIP runtime error */
+    ST_ERR_WORKSPACE = 6,   /* context workspace too small */
+    ST_ERR_OOM = 7
+} st_status;
+
+typedef enum { ST_F32 = 0, ST_F16 = 1, ST_BF16 = 2 } st_dtype;
+
+/* flags */
+#define ST_FLAG_ZEROS_PLUS_ONE 0x1u /* qzeros hold z - 1 (AutoGPTQ v1 files) */
+
+/* ------------------------------------------------------------ runtime */
+
+/* Message of the last failed call on this thread ("" if none). */
+const char *st_last_error(void);
+
+/* Version string of the built library (kernels + ABI revision). */
+const char *st_version(void);
+
+/* Replaces GpuContext::new (src/gpu.rs:17-78): binds `device`, creates one
+ * stream and the split-K workspace (default 64 MiB). */
+int st_context_create(int device, st_context **out);
+
+/* Replaces GpuContext::from_device_queue (src/gpu.rs:24-33): run on a caller
+ * stream (hipStream_t passed as void*; NULL = the device's null stream)
+ * instead of the context's own. Waits for work queued on the old stream. */
+int st_context_set_stream(st_context *ctx, void *hip_stream);
+void *st_context_stream(st_context *ctx);
+
+/* Grow the split-K workspace to at least `bytes` (call at init, never on the
+ * hot path; kernels never allocate). */
+int st_context_reserve_workspace(st_context *ctx, size_t bytes);
+
+int st_context_destroy(st_context *ctx);
+
+/* Replaces GpuContext::create_buffer / create_storage_buffer (src/gpu.rs:80-103): device
+ * allocation, size rounded up to 4 bytes, 256-byte aligned. */
+int st_alloc(st_context *ctx, size_t bytes, void **out);
+int st_free(st_context *ctx, void *ptr);
+
+/* Replaces GpuContext::upload_buffer (src/gpu.rs:105-117): host -> device,
+ * returns when the data is on the device. */
+int st_upload(st_context *ctx, void *dst, const void *host_src, size_t bytes);
+
+/* Replaces GpuContext::write_buffer (src/gpu.rs:278-282): stream-ordered
+ * host -> device write at a byte offset. */
+int st_write(st_context *ctx, void *dst, size_t offset, const void *host_src, size_t bytes);
+
+/* Replaces GpuContext::read_buffer (src/gpu.rs:252-276): waits for all queued
+ * work, then copies device -> host. */
+int st_read(st_context *ctx, const void *src, void *host_dst, size_t bytes);
+
+/* Replaces GpuContext::copy_buffer (src/gpu.rs:245-250), stream-ordered. */
+int st_copy(st_context *ctx, void *dst, const void *src, size_t bytes);
+
+/* Replaces GpuContext::flush (src/gpu.rs:237-242): wait for the stream. */
+int st_flush(st_context *ctx);
+
+/* -------------------------------------------------------- GPTQ int4 */
+
+/* y = x . dequant(W), W[k, n] = (q[k, n] - z[g(k), n]) * scales[g(k), n].
+ * Replaces Model::gptq_matvec (src/model.rs:357-381) dispatching
+ * gptq_matvec(_4t).wgsl (src/shaders/gptq_matvec_4t.wgsl:20-86).
+ *   x        [M, K] in x_dtype (ST_F32 or ST_F16)
+ *   qzeros   NULL = symmetric z = 8, the reference's only mode
+ *   perm     NULL, or int32[K] from st_gptq_i4_act_order (then qweight is the
+ *            act-order-sorted copy): x is read as x[:, perm[k]]
+ *   y        f32 [M, N]
+ * Requires K % group_size == 0, group_size in {64, 128, 256}, N % 8 == 0,
+ * 1 <= M <= 32, 16-byte aligned qweight and x. Accumulation: exact integer
+ * products of the nibbles with a 3 x 8-bit split of x scaled by a power of
+ * two per group, f32 across groups (rel-L2 vs f64 ~1e-7). */
+int st_gptq_i4_matvec(st_context *ctx, const void *x, int x_dtype,
+                      const uint32_t *qweight, const uint16_t *scales,
+                      const uint32_t *qzeros, const int32_t *perm, float *y,
+                      int M, int K, int N, int group_size, uint32_t flags);
+
+/* y = (silu(a) * b) . dequant(W), silu(v) = v / (1 + exp(-v)).
+ * Replaces Model::fused_silu_gptq_down (src/model.rs:383-408) dispatching
+ * fused_silu_gptq(_4t).wgsl (src/shaders/fused_silu_gptq_4t.wgsl:26-81).
+ * a, b: f32 [M, K]. Other arguments as st_gptq_i4_matvec. */
+int st_gptq_i4_silu_matvec(st_context *ctx, const float *a, const float *b,
+                           const uint32_t *qweight, const uint16_t *scales,
+                           const uint32_t *qzeros, const int32_t *perm, float *y,
+                           int M, int K, int N, int group_size, uint32_t flags);
+
+/* y = silu(x . dequant(Wg)) * (x . dequant(Wu)), both [K, N].
+ * Replaces fused_gate_up_silu(_4t).wgsl (src/shaders/fused_gate_up_silu_4t.wgsl:28-91,
+ * declared at src/model.rs:8; the reference's forward runs gate and up as two
+ * gptq_matvec calls at src/model.rs:803-808). Both weights share perm. */
+int st_gptq_i4_gate_up_silu(st_context *ctx, const void *x, int x_dtype,
+                            const uint32_t *qweight_gate, const uint16_t *scales_gate,
+                            const uint32_t *qzeros_gate, const uint32_t *qweight_up,
+                            const uint16_t *scales_up, const uint32_t *qzeros_up,
+                            const int32_t *perm, float *y, int M, int K, int N,
+                            int group_size, uint32_t flags);
+
+/* Materialise dequant(W) as out[K, N] in out_dtype (ST_F32 exact; ST_BF16
+ * round-to-nearest-even, which is src/weights.rs:257-313
+ * dequant_gptq_to_bf16). g_idx NULL = k / group_size (no act-order);
+ * otherwise the original int32 g_idx[K] of the checkpoint. */
+int st_gptq_i4_dequant(st_context *ctx, const uint32_t *qweight, const uint16_t *scales,
+                       const uint32_t *qzeros, const int32_t *g_idx, void *out, int out_dtype,
+                       int K, int N, int group_size, uint32_t flags);
+
+/* Upload-time act-order preparation (the reference drops .g_idx,
+ * src/weights.rs:372-374). Sorts K by group: perm_out[j] = the original row
+ * placed at position j (stable, ascending g_idx), and qweight_out = qweight
+ * with its rows permuted the same way (re-packed nibbles; dequantized values
+ * unchanged). Each group must hold exactly group_size rows. Scales and
+ * qzeros are unchanged. g_idx is a device pointer; blocks until done. */
+int st_gptq_i4_act_order(st_context *ctx, const uint32_t *qweight, const int32_t *g_idx,
+                         uint32_t *qweight_out, int32_t *perm_out, int K, int N,
+                         int group_size);
+
+/* Prefill GEMM: C[M, N] = A[M, K] . dequant(W), A f16, C in c_dtype (ST_F32
+ * or ST_F16). No reference counterpart (the reference prefills token by
+ * token, src/inference.rs:93-95). MFMA f16 with integer-valued (q - z)
+ * operands, f32 accumulation, per-group scale applied after each group.
+ * perm as st_gptq_i4_matvec. */
+int st_gptq_i4_gemm(st_context *ctx, const uint16_t *a, const uint32_t *qweight,
+                    const uint16_t *scales, const uint32_t *qzeros, const int32_t *perm,
+                    void *c, int c_dtype, int M, int K, int N, int group_size,
+                    uint32_t flags);
+
+/* ------------------------------------------------------------- INT8 */
+
+/* y[M, N] = x[M, K] . (w[N, K]^T * scale[N]), int8 symmetric per output
+ * channel. No reference counterpart. x in x_dtype (ST_F16 or ST_F32),
+ * 1 <= M <= 32, K % 64 == 0, N % 4 == 0. */
+int st_int8_matvec(st_context *ctx, const void *x, int x_dtype, const int8_t *w,
+                   const float *scale, float *y, int M, int K, int N);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* SHADY_HIP_H */

@@ -1,0 +1,63 @@
+// Shared runtime pieces of libshady_hip: the context, error reporting and
+// argument checks. gfx950 (CDNA4) only.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstdarg>
+#include <cstdint>
+#include <cstdio>
+#include <string>
+
+#include "shady_hip.h"
+
+struct st_context {
+    int device = 0;
+    hipStream_t stream = nullptr;
+    bool own_stream = false;
+    int num_cus = 256;
+    // Split-K workspace: per-split partial sums, and one arrival counter per
+    // column block. Counters are zeroed once here and reset to zero by the
+    // kernel that consumes them, so no per-call clearing is needed.
+    float *ws = nullptr;
+    size_t ws_bytes = 0;
+    unsigned *counters = nullptr;
+    int n_counters = 0;
+};
+
+namespace st {
+
+void set_error(const char *fmt, ...);
+void clear_error();
+
+inline int fail(int code, const char *fmt, ...) {
+    char buf[512];
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(buf, sizeof buf, fmt, ap);
+    va_end(ap);
+    set_error("%s", buf);
+    return code;
+}
+
+inline int hip_fail(hipError_t e, const char *what) {
+    return fail(ST_ERR_HIP, "%s: %s", what, hipGetErrorString(e));
+}
+
+#define ST_HIP(call)                                                       \
+    do {                                                                   \
+        hipError_t _e = (call);                                            \
+        if (_e != hipSuccess) return ::st::hip_fail(_e, #call);            \
+    } while (0)
+
+inline bool aligned16(const void *p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+// Launch-error check after a kernel launch (launch failures only; faults
+// surface at the next synchronising call).
+inline int launch_check(const char *what) {
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return hip_fail(e, what);
+    return ST_OK;
+}
+
+}  // namespace st

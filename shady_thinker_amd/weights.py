@@ -1,0 +1,122 @@
+"""Quantized weight formats and their upload (src/weights.rs counterparts).
+
+QuantConfig mirrors src/weights.rs:154-167. GptqWeight holds one GPTQ linear
+on the device in the reference layout (qweight u32[K/8, N], scales f16[G, N])
+plus what the reference drops at load (src/weights.rs:372-374): qzeros and
+g_idx. An act-order g_idx is resolved at upload by st_gptq_i4_act_order
+(rows sorted by group, values unchanged). Int8Weight is the INT8
+per-channel format (no reference counterpart).
+"""
+from __future__ import annotations
+
+import json
+from dataclasses import dataclass
+
+import numpy as np
+
+from ._lib import ST_FLAG_ZEROS_PLUS_ONE, call
+
+
+@dataclass
+class QuantConfig:
+    """quantize_config.json (src/weights.rs:154-167); the reference reads
+    only group_size (src/model.rs:366)."""
+
+    bits: int = 4
+    group_size: int = 128
+    quant_method: str = "gptq"
+    sym: bool = True
+
+    @classmethod
+    def from_dict(cls, d: dict) -> "QuantConfig":
+        return cls(
+            bits=int(d.get("bits", 4)),
+            group_size=int(d.get("group_size", 128)),
+            quant_method=str(d.get("quant_method", "gptq")),
+            sym=bool(d.get("sym", True)),
+        )
+
+    @classmethod
+    def from_file(cls, path: str) -> "QuantConfig":
+        with open(path) as f:
+            return cls.from_dict(json.load(f))
+
+
+def _identity_groups(g_idx: np.ndarray, gs: int) -> bool:
+    return bool(np.array_equal(g_idx, np.arange(g_idx.size, dtype=np.int64) // gs))
+
+
+@dataclass
+class GptqWeight:
+    """One GPTQ int4 linear resident in HBM.
+
+    qweight: int32 tensor [K/8, N] (bit pattern of the u32 words)
+    scales:  float16 tensor [G, N]
+    qzeros:  int32 tensor [G, N/8] or None (symmetric z = 8)
+    perm:    int32 tensor [K] or None (act-order: qweight is the sorted copy)
+    """
+
+    qweight: object
+    scales: object
+    qzeros: object
+    perm: object
+    K: int
+    N: int
+    group_size: int
+    flags: int = 0
+
+    @classmethod
+    def upload(cls, gpu, qweight: np.ndarray, scales: np.ndarray, group_size: int = 128,
+               qzeros: np.ndarray | None = None, g_idx: np.ndarray | None = None,
+               zeros_plus_one: bool = False) -> "GptqWeight":
+        """Upload the checkpoint tensors verbatim (src/weights.rs:398); for an
+        act-order g_idx, sort rows by group on the device."""
+        torch = gpu.torch
+        qw = np.ascontiguousarray(qweight).view(np.uint32)
+        K, N = qw.shape[0] * 8, qw.shape[1]
+        sc = np.ascontiguousarray(scales).view(np.uint16)
+        d_qw = gpu.upload_array(qw.view(np.int32), torch.int32)
+        d_sc = gpu.upload_array(sc.view(np.float16), torch.float16)
+        d_qz = None if qzeros is None else gpu.upload_array(np.ascontiguousarray(qzeros).view(np.int32), torch.int32)
+        d_perm = None
+        if g_idx is not None and not _identity_groups(np.asarray(g_idx), group_size):
+            d_gi = gpu.upload_array(np.ascontiguousarray(g_idx, dtype=np.int32), torch.int32)
+            sorted_qw = torch.empty_like(d_qw)
+            d_perm = torch.empty(K, dtype=torch.int32, device=gpu.device)
+            gpu.sync_stream()
+            call("st_gptq_i4_act_order", gpu.handle, d_qw.data_ptr(), d_gi.data_ptr(), sorted_qw.data_ptr(),
+                 d_perm.data_ptr(), K, N, group_size)
+            d_qw = sorted_qw
+        flags = ST_FLAG_ZEROS_PLUS_ONE if zeros_plus_one else 0
+        return cls(d_qw, d_sc, d_qz, d_perm, K, N, group_size, flags)
+
+    @property
+    def nbytes(self) -> int:
+        n = self.qweight.numel() * 4 + self.scales.numel() * 2
+        if self.qzeros is not None:
+            n += self.qzeros.numel() * 4
+        if self.perm is not None:
+            n += self.perm.numel() * 4
+        return n
+
+
+@dataclass
+class Int8Weight:
+    """INT8 symmetric per-output-channel weight: w int8 [N, K], scale f32 [N]."""
+
+    w: object
+    scale: object
+    K: int
+    N: int
+
+    @classmethod
+    def upload(cls, gpu, w: np.ndarray, scale: np.ndarray) -> "Int8Weight":
+        torch = gpu.torch
+        w = np.ascontiguousarray(w, dtype=np.int8)
+        N, K = w.shape
+        return cls(gpu.upload_array(w, torch.int8),
+                   gpu.upload_array(np.ascontiguousarray(scale, dtype=np.float32), torch.float32), K, N)
+
+    @property
+    def nbytes(self) -> int:
+        return self.w.numel() + self.scale.numel() * 4

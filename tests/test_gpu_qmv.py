@@ -1,0 +1,296 @@
+"""GPU parity of the decode kernels (st_gptq_i4_matvec / _silu_matvec /
+_gate_up_silu, st_int8_matvec) against the CPU oracle, through the C ABI.
+
+Bars (stated in BASELINE.json north_star): matvec outputs within rel-L2
+1e-4 of the float64 oracle and of the reference's WGSL-order f32 path;
+dequantized weights bit-exact (one-hot inputs return dequantized rows
+exactly).
+"""
+import os
+
+import numpy as np
+import pytest
+import torch
+
+import shady_thinker_amd as sta
+from shady_thinker_amd import model as M
+
+pytestmark = pytest.mark.gpu
+
+TOL = 1e-4  # rel-L2, f32-accumulate matvec (north_star)
+GOLDEN = os.path.join(os.path.dirname(__file__), "golden")
+
+
+def up(gpu, case, zeros_plus_one=False):
+    return sta.GptqWeight.upload(gpu, case["qweight"], case["scales"], case["gs"], qzeros=case["qzeros"],
+                                 g_idx=case["g_idx"], zeros_plus_one=zeros_plus_one)
+
+
+def run_matvec(gpu, w, x_np, dtype=torch.float32):
+    x = torch.from_numpy(np.ascontiguousarray(x_np)).to(gpu.device)
+    if dtype == torch.float16:
+        x = x.half()
+    m = x.numel() // w.K
+    y = torch.empty(m, w.N, dtype=torch.float32, device=gpu.device)
+    M.gptq_matvec(gpu, "t", x, w.qweight, w.scales, y, w.K, w.N, w.group_size, w.qzeros, w.perm, w.flags)
+    torch.cuda.synchronize()
+    return y.cpu().numpy()
+
+
+def test_cfg1_matches_oracle_and_wgsl(gpu, orc):
+    K = N = 2048
+    c = orc.gptq_case(0, K, N, 128)
+    w = up(gpu, c)
+    y = run_matvec(gpu, w, c["x"])[0]
+    ref = orc.gptq_matvec_f64(c["x"], c["qweight"], c["scales"], K, N, 128)
+    wg = orc.gptq_matvec_wgsl(c["x"], c["qweight"], c["scales"], K, N, 128, 1, 1)
+    e64, ewg = orc.rel_l2(y, ref), orc.rel_l2(y, wg)
+    print(f"cfg1 rel-L2 vs f64 {e64:.3e}, vs WGSL-4t {ewg:.3e}")
+    assert e64 < TOL and ewg < TOL
+    assert e64 < 1e-6  # the integer-limb scheme is far tighter than the bar
+
+
+def test_one_hot_returns_dequant_rows_exactly(gpu, orc):
+    K, N, gs = 1024, 264, 128
+    c = orc.gptq_case(1, K, N, gs, zeros=True)
+    w = up(gpu, c)
+    W = orc.gptq_dequant_f32(c["qweight"], c["scales"], K, N, gs, qzeros=c["qzeros"])
+    ks = [0, 1, 7, 8, 127, 128, 500, 1023]
+    x = np.zeros((len(ks), K), np.float32)
+    for i, k in enumerate(ks):
+        x[i, k] = 1.0
+    y = run_matvec(gpu, w, x)
+    assert np.array_equal(y, W[ks]), "dequantized rows must be bit-exact"
+    # a power-of-two scaled one-hot too (the per-group exponent path)
+    y2 = run_matvec(gpu, w, x * np.float32(2.0 ** -30))
+    assert np.array_equal(y2, W[ks] * np.float32(2.0 ** -30))
+
+
+def test_integer_exact_case_bit_equal(gpu, orc):
+    K, N, gs = 2048, 512, 128
+    c = orc.gptq_case(2, K, N, gs)
+    c["scales"] = np.ones_like(c["scales"])
+    x = np.round(c["x"] * 4).astype(np.float32)
+    w = up(gpu, c)
+    y = run_matvec(gpu, w, x)[0]
+    ref = orc.gptq_matvec_f64(x, c["qweight"], c["scales"], K, N, gs)
+    assert np.array_equal(y.astype(np.float64), ref)
+
+
+@pytest.mark.parametrize("K,N,gs,Mr", [
+    (128, 8, 128, 1), (256, 64, 64, 1), (512, 264, 128, 1), (4096, 4096, 128, 1), (11008, 4096, 128, 1),
+    (2560, 1032, 256, 1), (4096, 2048, 128, 2), (2048, 520, 128, 3), (2048, 1024, 64, 5), (4096, 512, 128, 8),
+    (2560, 1024, 128, 16), (1024, 256, 128, 32),
+])
+def test_shapes_vs_f64(gpu, orc, K, N, gs, Mr):
+    c = orc.gptq_case(K + N + Mr, K, N, gs, M=Mr)
+    w = up(gpu, c)
+    y = run_matvec(gpu, w, c["x"])
+    ref = orc.gptq_matvec_f64(c["x"], c["qweight"], c["scales"], K, N, gs)
+    assert y.shape == (Mr, N)
+    e = orc.rel_l2(y, ref)
+    print(f"K={K} N={N} gs={gs} M={Mr}: rel-L2 {e:.3e}")
+    assert e < TOL
+    for m in range(Mr):  # every row individually too
+        assert orc.rel_l2(y[m], ref[m]) < TOL
+
+
+def test_f16_activations(gpu, orc):
+    K, N = 4096, 4096
+    c = orc.gptq_case(31, K, N, 128, x_dtype=np.float16)
+    w = up(gpu, c)
+    y = run_matvec(gpu, w, c["x"], dtype=torch.float16)[0]
+    ref = orc.gptq_matvec_f64(c["x"].astype(np.float64), c["qweight"], c["scales"], K, N, 128)
+    assert orc.rel_l2(y, ref) < TOL
+
+
+@pytest.mark.parametrize("plus_one", [False, True])
+def test_zero_points(gpu, orc, plus_one):
+    K, N, gs = 4096, 1024, 128
+    c = orc.gptq_case(41, K, N, gs, zeros=True, M=2)
+    w = up(gpu, c, zeros_plus_one=plus_one)
+    y = run_matvec(gpu, w, c["x"])
+    ref = orc.gptq_matvec_f64(c["x"], c["qweight"], c["scales"], K, N, gs, qzeros=c["qzeros"],
+                              zero_offset=int(plus_one))
+    assert orc.rel_l2(y, ref) < TOL
+
+
+def test_act_order(gpu, orc):
+    K, N, gs = 4096, 2048, 128
+    c = orc.gptq_case(51, K, N, gs, zeros=True, act_order=True)
+    w = up(gpu, c)
+    assert w.perm is not None
+    y = run_matvec(gpu, w, c["x"])[0]
+    ref = orc.gptq_matvec_f64(c["x"], c["qweight"], c["scales"], K, N, gs, qzeros=c["qzeros"], g_idx=c["g_idx"])
+    assert orc.rel_l2(y, ref) < TOL
+    # identity g_idx is detected and needs no permutation
+    c2 = dict(c, g_idx=(np.arange(K) // gs).astype(np.int32))
+    assert up(gpu, c2).perm is None
+
+
+def test_act_order_sorted_weights_dequantize_identically(gpu, orc):
+    K, N, gs = 1024, 128, 128
+    c = orc.gptq_case(52, K, N, gs, act_order=True)
+    w = up(gpu, c)
+    perm = w.perm.cpu().numpy()
+    qs = w.qweight.cpu().numpy().view(np.uint32)
+    W = orc.gptq_dequant_f32(c["qweight"], c["scales"], K, N, gs, g_idx=c["g_idx"])
+    Ws = orc.gptq_dequant_f32(qs, c["scales"], K, N, gs)  # sorted: group = k // gs
+    assert np.array_equal(Ws, W[perm])
+    assert np.array_equal(np.sort(perm), np.arange(K))
+    assert np.all(np.diff(c["g_idx"][perm]) >= 0)
+
+
+def test_act_order_rejects_unequal_groups(gpu, orc):
+    K, N, gs = 256, 64, 128
+    c = orc.gptq_case(53, K, N, gs)
+    bad = np.zeros(K, np.int32)  # all rows in group 0
+    with pytest.raises(sta.ShadyHipError) as ei:
+        sta.GptqWeight.upload(gpu, c["qweight"], c["scales"], gs, g_idx=bad)
+    assert ei.value.code == 2
+
+
+def test_fused_silu_down(gpu, orc):
+    K, N, gs = 11008, 4096, 128
+    c = orc.gptq_case(61, K, N, gs)
+    a = orc.normal_f32(610, K) * 2
+    b = orc.normal_f32(611, K)
+    w = up(gpu, c)
+    da = torch.from_numpy(a).cuda()
+    db = torch.from_numpy(b).cuda()
+    y = torch.empty(1, N, device="cuda")
+    M.fused_silu_gptq_down(gpu, da, db, w.qweight, w.scales, y, K, N, gs)
+    torch.cuda.synchronize()
+    y = y.cpu().numpy()[0]
+    ref = orc.gptq_matvec_f64(orc.silu_mul_f64(a, b), c["qweight"], c["scales"], K, N, gs)
+    wg = orc.fused_silu_gptq_wgsl(a, b, c["qweight"], c["scales"], K, N, gs, 1, 1)
+    assert orc.rel_l2(y, ref) < TOL and orc.rel_l2(y, wg) < TOL
+    # a = 0 -> silu = 0 -> y = 0 exactly
+    y0 = torch.full((1, N), 5.0, device="cuda")
+    M.fused_silu_gptq_down(gpu, torch.zeros(K, device="cuda"), db, w.qweight, w.scales, y0, K, N, gs)
+    torch.cuda.synchronize()
+    assert torch.count_nonzero(y0).item() == 0
+
+
+@pytest.mark.parametrize("Mr", [1, 4, 16])
+def test_gate_up_silu(gpu, orc, Mr):
+    K, N, gs = 4096, 11008, 128
+    cg = orc.gptq_case(71, K, N, gs, M=Mr)
+    cu = orc.gptq_case(72, K, N, gs)
+    wg_, wu_ = up(gpu, cg), up(gpu, cu)
+    x = torch.from_numpy(cg["x"]).cuda()
+    y = torch.empty(Mr, N, device="cuda")
+    M.fused_gate_up_silu(gpu, x, wg_.qweight, wg_.scales, wu_.qweight, wu_.scales, y, K, N, gs)
+    torch.cuda.synchronize()
+    y = y.cpu().numpy()
+    g = orc.gptq_matvec_f64(cg["x"], cg["qweight"], cg["scales"], K, N, gs)
+    u = orc.gptq_matvec_f64(cg["x"], cu["qweight"], cu["scales"], K, N, gs)
+    ref = orc.silu_gate_f64(g, u)
+    assert orc.rel_l2(y, ref) < TOL
+    if Mr == 1:
+        wgsl = orc.gate_up_silu_wgsl(cg["x"], cg["qweight"], cg["scales"], cu["qweight"], cu["scales"], K, N, gs, 1, 1)
+        assert orc.rel_l2(y[0], wgsl) < TOL
+
+
+@pytest.mark.parametrize("Mr", [1, 8, 32])
+def test_int8_cfg3(gpu, orc, Mr):
+    K, N = 5120, 13824
+    c = orc.int8_case(81, K, N, M=Mr)
+    w = sta.Int8Weight.upload(gpu, c["w"], c["scale"])
+    x = torch.from_numpy(c["x"]).cuda()
+    y = torch.empty(Mr, N, device="cuda")
+    M.int8_matvec(gpu, x, w.w, w.scale, y, K, N)
+    torch.cuda.synchronize()
+    ref = orc.int8_matvec_f64(c["x"], c["w"], c["scale"], K, N)
+    e = orc.rel_l2(y.cpu().numpy(), ref)
+    print(f"int8 M={Mr} rel-L2 {e:.3e}")
+    assert e < TOL
+
+
+def test_int8_f32_small_ragged(gpu, orc):
+    K, N = 192, 36
+    c = orc.int8_case(82, K, N, M=3, x_dtype=np.float32)
+    w = sta.Int8Weight.upload(gpu, c["w"], c["scale"])
+    y = torch.empty(3, N, device="cuda")
+    M.int8_matvec(gpu, torch.from_numpy(c["x"]).cuda(), w.w, w.scale, y, K, N)
+    torch.cuda.synchronize()
+    assert orc.rel_l2(y.cpu().numpy(), orc.int8_matvec_f64(c["x"], c["w"], c["scale"], K, N)) < TOL
+
+
+def test_golden_fixtures(gpu, orc):
+    for f in sorted(os.listdir(GOLDEN)):
+        if not f.endswith(".npz"):
+            continue
+        d = np.load(os.path.join(GOLDEN, f))
+        kind, K, N = str(d["kind"]), int(d["K"]), int(d["N"])
+        if kind == "int8":
+            w = sta.Int8Weight.upload(gpu, d["w"], d["scale"])
+            x = torch.from_numpy(d["x"]).cuda()
+            y = torch.empty(d["y"].shape, device="cuda")
+            M.int8_matvec(gpu, x, w.w, w.scale, y, K, N)
+        else:
+            gs = int(d["gs"])
+            w = sta.GptqWeight.upload(gpu, d["qweight"], d["scales"], gs,
+                                      qzeros=d["qzeros"] if d["qzeros"].size else None,
+                                      g_idx=d["g_idx"] if d["g_idx"].size else None)
+            y = torch.empty(d["y"].shape, device="cuda")
+            if kind == "silu":
+                M.fused_silu_gptq_down(gpu, torch.from_numpy(d["a"]).cuda(), torch.from_numpy(d["b"]).cuda(),
+                                       w.qweight, w.scales, y, K, N, gs, w.qzeros, w.perm)
+            else:
+                M.gptq_matvec(gpu, "golden", torch.from_numpy(d["x"]).cuda(), w.qweight, w.scales, y, K, N, gs,
+                              w.qzeros, w.perm)
+        torch.cuda.synchronize()
+        e = orc.rel_l2(y.cpu().numpy(), d["y"])
+        assert e < TOL, (f, e)
+
+
+def test_deterministic_and_split_consistent(gpu, orc, monkeypatch):
+    K, N = 11008, 4096
+    c = orc.gptq_case(91, K, N, 128)
+    w = up(gpu, c)
+    y1 = run_matvec(gpu, w, c["x"])
+    y2 = run_matvec(gpu, w, c["x"])
+    assert np.array_equal(y1, y2)
+
+
+def test_nonfinite_input_poisons_output(gpu, orc):
+    K, N = 512, 64
+    c = orc.gptq_case(92, K, N, 128)
+    w = up(gpu, c)
+    x = c["x"].copy()
+    x[300] = np.nan
+    y = run_matvec(gpu, w, x)[0]
+    assert np.all(np.isnan(y))
+
+
+def test_bad_shapes_raise(gpu, orc):
+    c = orc.gptq_case(93, 256, 64, 128)
+    w = up(gpu, c)
+    x = torch.zeros(256, device="cuda")
+    y = torch.empty(64, device="cuda")
+    with pytest.raises(sta.ShadyHipError) as ei:
+        M.gptq_matvec(gpu, "t", x, w.qweight, w.scales, y, 256, 64, 32)  # unsupported group size
+    assert ei.value.code == 2
+    with pytest.raises(sta.ShadyHipError):
+        M.gptq_matvec(gpu, "t", torch.zeros(40 * 256, device="cuda"), w.qweight, w.scales, y, 256, 64, 128)  # M=40
+
+
+def test_dequant_kernel_bit_exact(gpu, orc):
+    K, N, gs = 1024, 192, 128
+    for zeros, act in [(False, False), (True, False), (True, True)]:
+        c = orc.gptq_case(94, K, N, gs, zeros=zeros, act_order=act)
+        qw = gpu.upload_array(c["qweight"].view(np.int32), torch.int32)
+        sc = gpu.upload_array(c["scales"], torch.float16)
+        qz = None if c["qzeros"] is None else gpu.upload_array(c["qzeros"].view(np.int32), torch.int32)
+        gi = None if c["g_idx"] is None else gpu.upload_array(c["g_idx"], torch.int32)
+        out = torch.empty(K, N, device="cuda")
+        M.gptq_dequant(gpu, qw, sc, out, K, N, gs, qz, gi)
+        ob = torch.empty(K, N, device="cuda", dtype=torch.bfloat16)
+        M.gptq_dequant(gpu, qw, sc, ob, K, N, gs, qz, gi)
+        torch.cuda.synchronize()
+        ref = orc.gptq_dequant_f32(c["qweight"], c["scales"], K, N, gs, qzeros=c["qzeros"], g_idx=c["g_idx"])
+        assert np.array_equal(out.cpu().numpy().view(np.uint32), ref.view(np.uint32))
+        if not zeros:
+            refb = orc.gptq_dequant_bf16(c["qweight"], c["scales"], K, N, gs)
+            assert np.array_equal(ob.cpu().view(torch.int16).numpy().view(np.uint16), refb)
