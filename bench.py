@@ -42,9 +42,18 @@ def decode_bytes(K, N, x_bytes, y_n, n_inputs=1):
     return K * N // 2 + 2 * (K // GS) * N + n_inputs * K * x_bytes + 4 * y_n
 
 
-def make_gptq(torch, dev, K, N, gen):
+def make_gptq(torch, dev, K, N, gen, gpu=None):
+    """Random GPTQ int4 weight (uniform nibbles, |N(0,0.02)| f16 scales); with
+    `gpu`, repacked into the decode kernels' tiled layout as an upload does."""
     qw = torch.randint(-(2**31), 2**31 - 1, (K // 8, N), dtype=torch.int32, device=dev, generator=gen)
     sc = (torch.randn(K // GS, N, device=dev, generator=gen) * 0.02).abs().half()
+    if gpu is not None:
+        from shady_thinker_amd._lib import call, lib
+
+        t = torch.empty(lib().st_gptq_i4_tiled_words(K, N, GS), dtype=torch.int32, device=dev)
+        gpu.sync_stream()
+        call("st_gptq_i4_repack", gpu.handle, qw.data_ptr(), t.data_ptr(), K, N, GS)
+        qw = t
     return qw, sc
 
 
@@ -141,11 +150,12 @@ def main():
     W = []
     for _ in range(copies):
         W.append({
-            "q": make_gptq(torch, dev, H, H, gen),
-            "g": make_gptq(torch, dev, H, I, gen),
-            "u": make_gptq(torch, dev, H, I, gen),
-            "d": make_gptq(torch, dev, I, H, gen),
+            "q": make_gptq(torch, dev, H, H, gen, gpu),
+            "g": make_gptq(torch, dev, H, I, gen, gpu),
+            "u": make_gptq(torch, dev, H, I, gen, gpu),
+            "d": make_gptq(torch, dev, I, H, gen, gpu),
         })
+    TF = sta._lib.ST_FLAG_TILED
     x = torch.randn(1, H, device=dev, generator=gen)
     yq = torch.empty(1, H, device=dev)
     a = torch.randn(1, I, device=dev, generator=gen)
@@ -155,15 +165,15 @@ def main():
 
     def k_q(i):
         w = W[i % copies]["q"]
-        Mdl.gptq_matvec(gpu, "q_proj", x, w[0], w[1], yq, H, H, GS)
+        Mdl.gptq_matvec(gpu, "q_proj", x, w[0], w[1], yq, H, H, GS, flags=TF)
 
     def k_gu(i):
         w = W[i % copies]
-        Mdl.fused_gate_up_silu(gpu, x, w["g"][0], w["g"][1], w["u"][0], w["u"][1], ygu, H, I, GS)
+        Mdl.fused_gate_up_silu(gpu, x, w["g"][0], w["g"][1], w["u"][0], w["u"][1], ygu, H, I, GS, flags=TF)
 
     def k_dn(i):
         w = W[i % copies]["d"]
-        Mdl.fused_silu_gptq_down(gpu, a, b, w[0], w[1], ydn, I, H, GS)
+        Mdl.fused_silu_gptq_down(gpu, a, b, w[0], w[1], ydn, I, H, GS, flags=TF)
 
     def step(i):
         k_q(i)

@@ -56,6 +56,7 @@ typedef enum { ST_F32 = 0, ST_F16 = 1, ST_BF16 = 2 } st_dtype;
 
 /* flags */
 #define ST_FLAG_ZEROS_PLUS_ONE 0x1u /* qzeros hold z - 1 (AutoGPTQ v1 files) */
+#define ST_FLAG_TILED 0x2u          /* qweight is in the tiled layout of st_gptq_i4_repack */
 
 /* ------------------------------------------------------------ runtime */
 
@@ -114,6 +115,7 @@ int st_flush(st_context *ctx);
  *   perm     NULL, or int32[K] from st_gptq_i4_act_order (then qweight is the
  *            act-order-sorted copy): x is read as x[:, perm[k]]
  *   y        f32 [M, N]
+ *   flags    ST_FLAG_ZEROS_PLUS_ONE, ST_FLAG_TILED (qweight from st_gptq_i4_repack)
  * Requires K % group_size == 0, group_size in {64, 128, 256}, N % 8 == 0,
  * 1 <= M <= 32, 16-byte aligned qweight and x. Accumulation: exact integer
  * products of the nibbles with a 3 x 8-bit split of x scaled by a power of
@@ -151,6 +153,17 @@ int st_gptq_i4_dequant(st_context *ctx, const uint32_t *qweight, const uint16_t 
                        const uint32_t *qzeros, const int32_t *g_idx, void *out, int out_dtype,
                        int K, int N, int group_size, uint32_t flags);
 
+/* Upload-time repack into the decode kernels' tiled layout (no reference
+ * counterpart; an optional step of the weight upload, src/weights.rs:398):
+ * per 16-column tile and group, the 64 lanes' words are contiguous, so the
+ * kernel reads 1 KiB contiguous per group with 128-bit loads. Dequantized
+ * values are unchanged (a permutation of whole words). qweight_tiled must hold
+ * st_gptq_i4_tiled_words(K, N, group_size) words; pass ST_FLAG_TILED to the
+ * matvec entry points with it. */
+size_t st_gptq_i4_tiled_words(int K, int N, int group_size);
+int st_gptq_i4_repack(st_context *ctx, const uint32_t *qweight, uint32_t *qweight_tiled, int K, int N,
+                      int group_size);
+
 /* Upload-time act-order preparation (the reference drops .g_idx,
  * src/weights.rs:372-374). Sorts K by group: perm_out[j] = the original row
  * placed at position j (stable, ascending g_idx), and qweight_out = qweight
@@ -175,7 +188,7 @@ int st_gptq_i4_gemm(st_context *ctx, const uint16_t *a, const uint32_t *qweight,
 
 /* y[M, N] = x[M, K] . (w[N, K]^T * scale[N]), int8 symmetric per output
  * channel. No reference counterpart. x in x_dtype (ST_F16 or ST_F32),
- * 1 <= M <= 32, K % 64 == 0, N % 4 == 0. */
+ * 1 <= M <= 32, K % 128 == 0, N % 4 == 0. */
 int st_int8_matvec(st_context *ctx, const void *x, int x_dtype, const int8_t *w,
                    const float *scale, float *y, int M, int K, int N);
 

@@ -17,6 +17,7 @@ HEADER = os.path.join(ROOT, "include", "shady_hip.h")
 ST_OK = 0
 ST_F32, ST_F16, ST_BF16 = 0, 1, 2
 ST_FLAG_ZEROS_PLUS_ONE = 0x1
+ST_FLAG_TILED = 0x2
 
 STATUS_NAMES = {
     0: "ST_OK", 1: "ST_ERR_INVALID", 2: "ST_ERR_SHAPE", 3: "ST_ERR_ALIGN",
@@ -59,6 +60,8 @@ _SIGNATURES = {
     "st_gptq_i4_gate_up_silu": (_I, [_P, _P, _I, _P, _P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _U32]),
     "st_gptq_i4_dequant": (_I, [_P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _U32]),
     "st_gptq_i4_act_order": (_I, [_P, _P, _P, _P, _P, _I, _I, _I]),
+    "st_gptq_i4_tiled_words": (_SZ, [_I, _I, _I]),
+    "st_gptq_i4_repack": (_I, [_P, _P, _P, _I, _I, _I]),
     "st_gptq_i4_gemm": (_I, [_P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _U32]),
     "st_int8_matvec": (_I, [_P, _P, _I, _P, _P, _P, _I, _I, _I]),
 }

@@ -16,7 +16,10 @@ ROOT = os.path.dirname(HERE)
 CSRC = os.path.join(HERE, "csrc")
 OBJ = os.path.join(HERE, "_build")
 LIB = os.path.join(HERE, "libshady_hip.so")
-SOURCES = ["runtime.hip", "qmv.hip", "dequant.hip", "gemm.hip"]
+SOURCES = [
+    "runtime.hip", "qmv.hip", "qmv_i4_p0.hip", "qmv_i4_p1.hip", "qmv_i4t_p0.hip", "qmv_i4t_p1.hip", "qmv_i8.hip",
+    "dequant.hip", "gemm.hip",
+]
 
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 FLAGS = [
@@ -52,7 +55,7 @@ def build(verbose: bool = True) -> str:
     """Compile every HIP source (always) and link libshady_hip.so."""
     os.makedirs(OBJ, exist_ok=True)
     srcs = [s for s in SOURCES if os.path.exists(os.path.join(CSRC, s))]
-    with cf.ThreadPoolExecutor(max_workers=min(4, len(srcs))) as ex:
+    with cf.ThreadPoolExecutor(max_workers=min(8, len(srcs))) as ex:
         objs = list(ex.map(_compile, srcs))
     tmp = LIB + ".tmp"
     cmd = [HIPCC, "--offload-arch=gfx950", "-shared", "-fPIC", *objs, "-o", tmp]

@@ -14,7 +14,7 @@ from dataclasses import dataclass
 
 import numpy as np
 
-from ._lib import ST_FLAG_ZEROS_PLUS_ONE, call
+from ._lib import ST_FLAG_TILED, ST_FLAG_ZEROS_PLUS_ONE, call, lib
 
 
 @dataclass
@@ -50,7 +50,8 @@ def _identity_groups(g_idx: np.ndarray, gs: int) -> bool:
 class GptqWeight:
     """One GPTQ int4 linear resident in HBM.
 
-    qweight: int32 tensor [K/8, N] (bit pattern of the u32 words)
+    qweight: int32 tensor, [K/8, N] (bit pattern of the u32 words) or, with
+             ST_FLAG_TILED in flags, the tiled layout of st_gptq_i4_repack
     scales:  float16 tensor [G, N]
     qzeros:  int32 tensor [G, N/8] or None (symmetric z = 8)
     perm:    int32 tensor [K] or None (act-order: qweight is the sorted copy)
@@ -68,9 +69,11 @@ class GptqWeight:
     @classmethod
     def upload(cls, gpu, qweight: np.ndarray, scales: np.ndarray, group_size: int = 128,
                qzeros: np.ndarray | None = None, g_idx: np.ndarray | None = None,
-               zeros_plus_one: bool = False) -> "GptqWeight":
+               zeros_plus_one: bool = False, tiled: bool = True) -> "GptqWeight":
         """Upload the checkpoint tensors verbatim (src/weights.rs:398); for an
-        act-order g_idx, sort rows by group on the device."""
+        act-order g_idx, sort rows by group on the device; with `tiled`,
+        repack qweight into the decode kernels' tiled layout (values
+        unchanged); otherwise keep the [K/8, N] reference layout."""
         torch = gpu.torch
         qw = np.ascontiguousarray(qweight).view(np.uint32)
         K, N = qw.shape[0] * 8, qw.shape[1]
@@ -88,7 +91,18 @@ class GptqWeight:
                  d_perm.data_ptr(), K, N, group_size)
             d_qw = sorted_qw
         flags = ST_FLAG_ZEROS_PLUS_ONE if zeros_plus_one else 0
+        if tiled:
+            words = lib().st_gptq_i4_tiled_words(K, N, group_size)
+            d_t = torch.empty(words, dtype=torch.int32, device=gpu.device)
+            gpu.sync_stream()
+            call("st_gptq_i4_repack", gpu.handle, d_qw.data_ptr(), d_t.data_ptr(), K, N, group_size)
+            d_qw = d_t
+            flags |= ST_FLAG_TILED
         return cls(d_qw, d_sc, d_qz, d_perm, K, N, group_size, flags)
+
+    @property
+    def tiled(self) -> bool:
+        return bool(self.flags & ST_FLAG_TILED)
 
     @property
     def nbytes(self) -> int:

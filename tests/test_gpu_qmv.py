@@ -21,9 +21,9 @@ TOL = 1e-4  # rel-L2, f32-accumulate matvec (north_star)
 GOLDEN = os.path.join(os.path.dirname(__file__), "golden")
 
 
-def up(gpu, case, zeros_plus_one=False):
+def up(gpu, case, zeros_plus_one=False, tiled=True):
     return sta.GptqWeight.upload(gpu, case["qweight"], case["scales"], case["gs"], qzeros=case["qzeros"],
-                                 g_idx=case["g_idx"], zeros_plus_one=zeros_plus_one)
+                                 g_idx=case["g_idx"], zeros_plus_one=zeros_plus_one, tiled=tiled)
 
 
 def run_matvec(gpu, w, x_np, dtype=torch.float32):
@@ -131,7 +131,7 @@ def test_act_order(gpu, orc):
 def test_act_order_sorted_weights_dequantize_identically(gpu, orc):
     K, N, gs = 1024, 128, 128
     c = orc.gptq_case(52, K, N, gs, act_order=True)
-    w = up(gpu, c)
+    w = up(gpu, c, tiled=False)
     perm = w.perm.cpu().numpy()
     qs = w.qweight.cpu().numpy().view(np.uint32)
     W = orc.gptq_dequant_f32(c["qweight"], c["scales"], K, N, gs, g_idx=c["g_idx"])
@@ -159,7 +159,7 @@ def test_fused_silu_down(gpu, orc):
     da = torch.from_numpy(a).cuda()
     db = torch.from_numpy(b).cuda()
     y = torch.empty(1, N, device="cuda")
-    M.fused_silu_gptq_down(gpu, da, db, w.qweight, w.scales, y, K, N, gs)
+    M.fused_silu_gptq_down(gpu, da, db, w.qweight, w.scales, y, K, N, gs, flags=w.flags)
     torch.cuda.synchronize()
     y = y.cpu().numpy()[0]
     ref = orc.gptq_matvec_f64(orc.silu_mul_f64(a, b), c["qweight"], c["scales"], K, N, gs)
@@ -167,7 +167,7 @@ def test_fused_silu_down(gpu, orc):
     assert orc.rel_l2(y, ref) < TOL and orc.rel_l2(y, wg) < TOL
     # a = 0 -> silu = 0 -> y = 0 exactly
     y0 = torch.full((1, N), 5.0, device="cuda")
-    M.fused_silu_gptq_down(gpu, torch.zeros(K, device="cuda"), db, w.qweight, w.scales, y0, K, N, gs)
+    M.fused_silu_gptq_down(gpu, torch.zeros(K, device="cuda"), db, w.qweight, w.scales, y0, K, N, gs, flags=w.flags)
     torch.cuda.synchronize()
     assert torch.count_nonzero(y0).item() == 0
 
@@ -180,7 +180,7 @@ def test_gate_up_silu(gpu, orc, Mr):
     wg_, wu_ = up(gpu, cg), up(gpu, cu)
     x = torch.from_numpy(cg["x"]).cuda()
     y = torch.empty(Mr, N, device="cuda")
-    M.fused_gate_up_silu(gpu, x, wg_.qweight, wg_.scales, wu_.qweight, wu_.scales, y, K, N, gs)
+    M.fused_gate_up_silu(gpu, x, wg_.qweight, wg_.scales, wu_.qweight, wu_.scales, y, K, N, gs, flags=wg_.flags)
     torch.cuda.synchronize()
     y = y.cpu().numpy()
     g = orc.gptq_matvec_f64(cg["x"], cg["qweight"], cg["scales"], K, N, gs)
@@ -208,7 +208,7 @@ def test_int8_cfg3(gpu, orc, Mr):
 
 
 def test_int8_f32_small_ragged(gpu, orc):
-    K, N = 192, 36
+    K, N = 384, 36
     c = orc.int8_case(82, K, N, M=3, x_dtype=np.float32)
     w = sta.Int8Weight.upload(gpu, c["w"], c["scale"])
     y = torch.empty(3, N, device="cuda")
@@ -236,10 +236,10 @@ def test_golden_fixtures(gpu, orc):
             y = torch.empty(d["y"].shape, device="cuda")
             if kind == "silu":
                 M.fused_silu_gptq_down(gpu, torch.from_numpy(d["a"]).cuda(), torch.from_numpy(d["b"]).cuda(),
-                                       w.qweight, w.scales, y, K, N, gs, w.qzeros, w.perm)
+                                       w.qweight, w.scales, y, K, N, gs, w.qzeros, w.perm, w.flags)
             else:
                 M.gptq_matvec(gpu, "golden", torch.from_numpy(d["x"]).cuda(), w.qweight, w.scales, y, K, N, gs,
-                              w.qzeros, w.perm)
+                              w.qzeros, w.perm, w.flags)
         torch.cuda.synchronize()
         e = orc.rel_l2(y.cpu().numpy(), d["y"])
         assert e < TOL, (f, e)
@@ -270,10 +270,11 @@ def test_bad_shapes_raise(gpu, orc):
     x = torch.zeros(256, device="cuda")
     y = torch.empty(64, device="cuda")
     with pytest.raises(sta.ShadyHipError) as ei:
-        M.gptq_matvec(gpu, "t", x, w.qweight, w.scales, y, 256, 64, 32)  # unsupported group size
+        M.gptq_matvec(gpu, "t", x, w.qweight, w.scales, y, 256, 64, 32, flags=w.flags)  # unsupported group size
     assert ei.value.code == 2
     with pytest.raises(sta.ShadyHipError):
-        M.gptq_matvec(gpu, "t", torch.zeros(40 * 256, device="cuda"), w.qweight, w.scales, y, 256, 64, 128)  # M=40
+        M.gptq_matvec(gpu, "t", torch.zeros(40 * 256, device="cuda"), w.qweight, w.scales, y, 256, 64, 128,
+                      flags=w.flags)  # M=40
 
 
 def test_dequant_kernel_bit_exact(gpu, orc):
@@ -294,3 +295,34 @@ def test_dequant_kernel_bit_exact(gpu, orc):
         if not zeros:
             refb = orc.gptq_dequant_bf16(c["qweight"], c["scales"], K, N, gs)
             assert np.array_equal(ob.cpu().view(torch.int16).numpy().view(np.uint16), refb)
+
+
+@pytest.mark.parametrize("K,N,gs,Mr,zeros", [(4096, 4096, 128, 1, False), (2048, 264, 64, 3, True),
+                                             (2560, 1032, 256, 5, False), (1024, 136, 128, 16, True)])
+def test_reference_and_tiled_layouts_agree(gpu, orc, K, N, gs, Mr, zeros):
+    """Both layouts give the same group results; only the split of K among
+    waves (hence the f32 order of the cross-wave sum) may differ."""
+    c = orc.gptq_case(K + Mr, K, N, gs, zeros=zeros, M=Mr)
+    yr = run_matvec(gpu, up(gpu, c, tiled=False), c["x"])
+    yt = run_matvec(gpu, up(gpu, c, tiled=True), c["x"])
+    assert orc.rel_l2(yr, yt) < 1e-6
+    assert orc.rel_l2(yt, orc.gptq_matvec_f64(c["x"], c["qweight"], c["scales"], K, N, gs, qzeros=c["qzeros"])) < TOL
+
+
+def test_repack_layout(gpu, orc):
+    """Tiled word ((T*G + g)*64 + lane)*(gs/32) + 2*st + h holds qweight
+    [g*gs/8 + 8*st + 2*(lane//16) + h][16*T + lane%16] (columns clamped)."""
+    K, N, gs = 512, 40, 128
+    c = orc.gptq_case(3, K, N, gs)
+    w = up(gpu, c, tiled=True)
+    got = w.qweight.cpu().numpy().view(np.uint32)
+    G, T, wpl = K // gs, (N + 15) // 16, gs // 32
+    assert got.size == T * 16 * K // 8
+    exp = np.empty_like(got)
+    for t in range(T):
+        for g in range(G):
+            for lane in range(64):
+                for j in range(wpl):
+                    pr = g * gs // 8 + 8 * (j // 2) + 2 * (lane // 16) + (j % 2)
+                    exp[((t * G + g) * 64 + lane) * wpl + j] = c["qweight"][pr, min(16 * t + lane % 16, N - 1)]
+    assert np.array_equal(got, exp)
