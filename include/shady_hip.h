@@ -72,7 +72,8 @@ int st_context_create(int device, st_context **out);
 
 /* Replaces GpuContext::from_device_queue (src/gpu.rs:24-33): run on a caller
  * stream (hipStream_t passed as void*; NULL = the device's null stream)
- * instead of the context's own. Waits for work queued on the old stream. */
+ * instead of the context's own. Does not synchronise (ordering between the
+ * old and the new stream is the caller's); legal during stream capture. */
 int st_context_set_stream(st_context *ctx, void *hip_stream);
 void *st_context_stream(st_context *ctx);
 

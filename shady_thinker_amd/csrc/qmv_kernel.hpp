@@ -56,7 +56,6 @@ typedef int v4i __attribute__((ext_vector_type(4)));
 typedef unsigned u32x4 __attribute__((ext_vector_type(4)));
 typedef unsigned u32x2 __attribute__((ext_vector_type(2)));
 
-constexpr int kMaxWaves = 16;  // waves per workgroup
 constexpr int kTileN = 16;     // output columns per workgroup (per source)
 constexpr int kMaxZeroUnits = 64;  // groups per wave whose zero points fit the LDS table
 
@@ -84,7 +83,10 @@ struct Params {
     int nwaves;    // waves per workgroup (K is split among them)
 };
 
-__device__ __forceinline__ float silu_f(float v) { return v / (1.0f + expf(-v)); }
+// silu(v) = v / (1 + exp(-v)) (fused_silu_gptq.wgsl:19-21), with the hardware
+// exp and reciprocal (a few ulp; WGSL's exp and division are not correctly
+// rounded either).
+__device__ __forceinline__ float silu_f(float v) { return __fdividef(v, 1.0f + __expf(-v)); }
 
 // k offset, within a lane's 16-k chunk, of int8 operand byte J for GPTQ:
 // register r = J/4 holds nibbles 2(J%4) (+1 for odd r) of word r/2.
@@ -164,33 +166,43 @@ __device__ __forceinline__ unsigned pack4(unsigned a, unsigned b, unsigned c, un
 // s_waitcnt vmcnt(0) (expcnt and lgkmcnt left at their maxima).
 __device__ __forceinline__ void wait_vm_all() { __builtin_amdgcn_s_waitcnt(0x0F70); }
 
-// Up to 16 waves per workgroup (128 VGPRs) only where the kernel fits that
-// budget without spilling; the rest run 4 waves (256 VGPRs).
-template <int FMT, int NSRC, int MB>
-constexpr bool kWide = MB == 1 && NSRC == 1 && FMT != FMT_I4;
+// Workgroup shapes. COOP kernels stage the whole K slice of x once per
+// workgroup into shared LDS with every lane of every wave, behind one
+// barrier (single-block tokens, when the slice fits); up to 16 waves for one
+// source (128 VGPRs each) or 8 for two. The fallback stages per wave, in
+// chunks, with 4 waves (256 VGPRs).
+template <int NSRC, bool COOP>
+constexpr int kMaxWavesFor = COOP ? (NSRC == 1 ? 16 : 8) : 4;
 
-// Prefetch ring depth: about 32 registers of weights in flight per lane.
-template <int FMT, int NSRC, int SPU>
+constexpr int kCoopRounds = 2;  // x staging rounds per lane in COOP kernels (bounds M * K)
+
+// Prefetch ring depth: the registers of weights in flight per lane, about 24
+// under a 128-VGPR budget (16-wave workgroups) and 40 for the dual kernel
+// (3 waves per SIMD, so every gate/up tile of a 7B layer is resident at once).
+template <int FMT, int NSRC, int SPU, bool COOP>
 constexpr int ring_depth() {
     constexpr int WPU = (FMT == FMT_I8) ? 4 * SPU : 2 * SPU;
     constexpr int RPU = NSRC * (WPU + (FMT == FMT_I8 ? 0 : 1));
-    return (32 / RPU) < 2 ? 2 : (32 / RPU);
+    constexpr int budget = (COOP && NSRC == 2) ? 40 : 24;
+    return (budget / RPU) < 2 ? 2 : ((budget / RPU) > 6 ? 6 : (budget / RPU));
 }
 
-template <int FMT, int NSRC, int XM, int MB, int SPU, bool PERM>
-__global__ __launch_bounds__((kWide<FMT, NSRC, MB> ? 64 * kMaxWaves : 256)) void qmv_kernel(Params p) {
+template <int FMT, int NSRC, int XM, int MB, int SPU, bool PERM, bool COOP>
+__global__ __launch_bounds__((64 * kMaxWavesFor<NSRC, COOP>)) void qmv_kernel(Params p) {
     extern __shared__ __align__(16) unsigned char smem[];
-    constexpr int D = ring_depth<FMT, NSRC, SPU>();
+    constexpr int D = ring_depth<FMT, NSRC, SPU, COOP>();
     constexpr int IPU = 4 * SPU;                              // 16-k items per group and token
     constexpr int WPU = (FMT == FMT_I8) ? 4 * SPU : 2 * SPU;  // weight dwords per lane per group
-    constexpr int RMAX = (4 * MB * IPU + 63) / 64;            // staging rounds per chunk (max)
+    // staging rounds per lane: per-wave chunk (fallback) or whole slice (COOP)
+    constexpr int RMAX = COOP ? kCoopRounds : (4 * MB * IPU + 63) / 64;
 
     const int tid = threadIdx.x;
     const int lane = tid & 63;
     const int wave = tid >> 6;
     const int q = lane >> 4;  // k-chunk of the operands; token within a 4-token block
     const int c = lane & 15;  // A row / B column
-    const int M = p.M, K = p.K, N = p.N, RB = p.rb, CH = p.chunk;
+    const int M = p.M, K = p.K, N = p.N, RB = p.rb;
+    const int NW = p.nwaves;
 
     // Workgroups are dealt to the 8 XCDs round-robin; give each XCD a
     // contiguous run of tiles so neighbouring tiles share L2 lines.
@@ -199,32 +211,38 @@ __global__ __launch_bounds__((kWide<FMT, NSRC, MB> ? 64 * kMaxWaves : 256)) void
     const int n0 = tile * kTileN;
     const int ncol = min(n0 + c, N - 1);  // clamped column this lane loads
 
-    const int NW = p.nwaves;
     const int u0 = (int)((long long)wave * p.units / NW);
     const int u1 = (int)((long long)(wave + 1) * p.units / NW);
 
-    // Per-wave LDS: A operands [chunk unit][step][mb][q][row], per
-    // (chunk unit, token) 2^-e, -H, -L (sum(X) = H*65536 + L), and the zero
-    // point table [unit][column] (GPTQ only).
-    u32x4 *abuf = reinterpret_cast<u32x4 *>(smem + (size_t)wave * p.wave_lds);
+    // LDS: A operands [unit][step][mb][q][row] (16 B each), per (unit, token)
+    // 2^-e, -H, -L (sum(X) = H*65536 + L), zero points [unit][src][column].
+    // COOP: one region for the workgroup, units = all groups; fallback: one
+    // region per wave, units = one chunk (zero table: the wave's groups).
+    const int CH = COOP ? p.units : p.chunk;  // units staged at once
+    const int ZU = COOP ? p.units : (u1 - u0);
+    unsigned char *region = smem + (COOP ? 0 : (size_t)wave * p.wave_lds);
+    u32x4 *abuf = reinterpret_cast<u32x4 *>(region);
     const int afrags = CH * SPU * MB * 4 * RB;
     float *s_em = reinterpret_cast<float *>(abuf + afrags);
     int *s_nh = reinterpret_cast<int *>(s_em + CH * M);
     int *s_nl = s_nh + CH * M;
     unsigned char *s_z = reinterpret_cast<unsigned char *>(s_nl + CH * M);
+    const int zbase = COOP ? 0 : u0;  // unit index of s_z row 0
 
     // ------------------------------------------- zero points (before all loads)
     bool have_z[NSRC];
 #pragma unroll
     for (int src = 0; src < NSRC; ++src) have_z[src] = FMT != FMT_I8 && p.qz[src] != nullptr;
     if constexpr (FMT != FMT_I8) {
-        if (have_z[0] && u0 < u1) {
-            for (int i = q; i < (u1 - u0); i += 4)
-#pragma unroll
-                for (int src = 0; src < NSRC; ++src) {
-                    const unsigned w = p.qz[src][(size_t)(u0 + i) * (N >> 3) + (ncol >> 3)];
-                    s_z[(i * NSRC + src) * 16 + c] = (unsigned char)(((w >> (4 * (ncol & 7))) & 0xF) + p.zoff);
-                }
+        if (have_z[0]) {
+            const int nz = ZU * NSRC * 16;
+            const int first = COOP ? tid : lane, stride = COOP ? 64 * NW : 64;
+            for (int i = first; i < nz; i += stride) {
+                const int col = i & 15, src = (i >> 4) % NSRC, uz = i / (16 * NSRC);
+                const int zc = min(n0 + col, N - 1);
+                const unsigned w = p.qz[src][(size_t)(zbase + uz) * (N >> 3) + (zc >> 3)];
+                s_z[i] = (unsigned char)(((w >> (4 * (zc & 7))) & 0xF) + p.zoff);
+            }
             wait_vm_all();  // nothing may be in flight across this branch
         }
     }
@@ -279,36 +297,45 @@ __global__ __launch_bounds__((kWide<FMT, NSRC, MB> ? 64 * kMaxWaves : 256)) void
     Unit ring[D];
 
     // ------------------------------------------------------ x staging
-    // Round r of a chunk starting at group cs: item i = 64r + lane covers
-    // token m = i / (CH*IPU), group cs + (i % (CH*IPU)) / IPU, 16 k of it.
-    // Every lane loads in every round (absent items read a clamped valid
-    // address).
+    // Round r covers items i = r * span + t (t = thread index in the staging
+    // group: the workgroup for COOP, the wave otherwise). Item i is token
+    // m = i / (CH*IPU), group cs + (i % (CH*IPU)) / IPU, 16 k of it. Every
+    // thread loads in every round (absent items read a clamped valid address).
+    const int span = COOP ? 64 * NW : 64;
+    const int tt = COOP ? tid : lane;
+    const int uend = COOP ? p.units : u1;  // staged groups end here
     float xv[RMAX][16];
     const int items = M * CH * IPU;
+    // A wave with no item in a round skips it (loads and work): the branch
+    // is uniform per wave and the same condition guards the loads and their
+    // only consumer, stage().
+    const int wfirst = COOP ? wave * 64 : 0;
     auto xload = [&](int cs) {
 #pragma unroll
         for (int r = 0; r < RMAX; ++r) {
-            const int i = min(64 * r + lane, items - 1);
+            if (r * span + wfirst >= items) continue;
+            const int i = min(r * span + tt, items - 1);
             const int m = i / (CH * IPU), w = i - m * (CH * IPU);
-            const int u = min(cs + w / IPU, u1 - 1);
+            const int u = min(cs + w / IPU, uend - 1);
             load_x16<XM, PERM>(p, m, u * p.gs + 16 * (w % IPU), xv[r]);
         }
     };
     auto stage = [&](int cs) {
 #pragma unroll
         for (int r = 0; r < RMAX; ++r) {
-            if (64 * r >= items) continue;  // uniform
-            const int i = 64 * r + lane;
+            if (r * span + wfirst >= items) continue;  // uniform per wave
+            const int i = r * span + tt;
             const int m = i / (CH * IPU), w = i - m * (CH * IPU);
             const int ui = w / IPU, ii = w % IPU;
-            const bool ok = i < items && cs + ui < u1;
-            float amax = 0.0f;
+            const bool ok = i < items && cs + ui < uend;
+            float amax = 0.0f, nf = 0.0f;
 #pragma unroll
             for (int j = 0; j < 16; ++j) {
-                // a non-finite x (NaN or inf) poisons its group: amax = inf -> y = NaN
-                const float a = fabsf(xv[r][j]);
-                amax = (a == a && a < INFINITY) ? fmaxf(amax, a) : INFINITY;
+                amax = fmaxf(amax, fabsf(xv[r][j]));
+                nf = fmaf(xv[r][j], 0.0f, nf);  // NaN iff some x is NaN or inf
             }
+            // a non-finite x poisons its group: amax = inf -> 2^-e = NaN -> y = NaN
+            amax = (nf == nf) ? amax : INFINITY;
             if (!ok) amax = 0.0f;
 #pragma unroll
             for (int o = 1; o < IPU; o <<= 1) amax = fmaxf(amax, __shfl_xor(amax, o));
@@ -326,8 +353,8 @@ __global__ __launch_bounds__((kWide<FMT, NSRC, MB> ? 64 * kMaxWaves : 256)) void
             int sum = 0;
 #pragma unroll
             for (int j = 0; j < 16; ++j) {
-                const float v = xv[r][j] * sc2;
-                X[j] = (ok && v == v && fabsf(v) < 8388608.0f) ? __float2int_rn(v) : 0;
+                // |x| 2^e < 2^22 when amax is finite; otherwise the group is NaN anyway
+                X[j] = __float2int_rn(xv[r][j] * sc2);
                 sum += X[j];
             }
 #pragma unroll
@@ -364,7 +391,7 @@ __global__ __launch_bounds__((kWide<FMT, NSRC, MB> ? 64 * kMaxWaves : 256)) void
     };
 
     // zero the A buffer once: rows 4t+3 and rows of absent tokens stay zero
-    for (int i = lane; i < afrags; i += 64) abuf[i] = u32x4{0, 0, 0, 0};
+    for (int i = tt; i < afrags; i += span) abuf[i] = u32x4{0, 0, 0, 0};
 
     // --------------------------------------------------------- main loop
     float tot[NSRC][MB];
@@ -418,7 +445,7 @@ __global__ __launch_bounds__((kWide<FMT, NSRC, MB> ? 64 * kMaxWaves : 256)) void
                     f = em;
                 } else {
                     f = (float)__builtin_bit_cast(_Float16, U.s[src]) * em;
-                    z = have_z[src] ? (int)s_z[((u - u0) * NSRC + src) * 16 + c] : 8;
+                    z = have_z[src] ? (int)s_z[((u - zbase) * NSRC + src) * 16 + c] : 8;
                 }
                 const int hi = S.x + __mul24(z, nh);
                 const int lo = (S.y << 8) + S.z + __mul24(z, nl);
@@ -427,35 +454,34 @@ __global__ __launch_bounds__((kWide<FMT, NSRC, MB> ? 64 * kMaxWaves : 256)) void
         }
     };
 
-    // At a chunk change (only when a wave's range exceeds one chunk) the new
-    // x loads are waited for at once, so no load count differs across the
-    // branch that issued them.
+    // Fallback only: at a chunk change (a wave's range exceeds one chunk:
+    // several tokens and a long K) the chunk's x is loaded, waited for and
+    // staged at once, so no load count differs across the branch and x is
+    // not held in registers across the main loop.
     auto next_chunk = [&](int u) {
+        xload(u);
+        wait_vm_all();
         stage(u);
-        if (u + CH < u1) {
-            xload(u + CH);
-            wait_vm_all();
-        }
     };
 
     // x first (loads complete in issue order, so the x slice must not queue
     // behind the weight ring), then the ring, all unconditionally.
+    const int cs0 = COOP ? 0 : u0;
+    if (COOP || u0 < u1) xload(cs0);
     if (u0 < u1) {
-        xload(u0);
 #pragma unroll
         for (int d = 0; d < D; ++d) load_unit(ring[d], min(u0 + d, u1 - 1));
-        stage(u0);
-        if (u0 + CH < u1) {
-            xload(u0 + CH);
-            wait_vm_all();
-        }
-        int ui = 0;  // group index within the current chunk
+    }
+    if (COOP || u0 < u1) stage(cs0);
+    if constexpr (COOP) __syncthreads();
+    if (u0 < u1) {
+        int ui = COOP ? u0 : 0;  // A-buffer index of the current group
         int base = u0;
         for (; base + D <= u1; base += D) {
 #pragma unroll
             for (int d = 0; d < D; ++d) {
                 const int u = base + d;
-                if (ui == CH) {
+                if (!COOP && ui == CH) {
                     ui = 0;
                     next_chunk(u);
                 }
@@ -468,7 +494,7 @@ __global__ __launch_bounds__((kWide<FMT, NSRC, MB> ? 64 * kMaxWaves : 256)) void
         for (int d = 0; d < D; ++d) {  // tail: fewer than D groups left, all in the ring
             const int u = base + d;
             if (u < u1) {
-                if (ui == CH) {
+                if (!COOP && ui == CH) {
                     ui = 0;
                     next_chunk(u);
                 }
@@ -479,7 +505,7 @@ __global__ __launch_bounds__((kWide<FMT, NSRC, MB> ? 64 * kMaxWaves : 256)) void
     }
 
     // ------------------------------------------- reduce the waves, write y
-    float *red = reinterpret_cast<float *>(smem + (size_t)NW * p.wave_lds);
+    float *red = reinterpret_cast<float *>(smem + (COOP ? (size_t)p.wave_lds : (size_t)NW * p.wave_lds));
 #pragma unroll
     for (int src = 0; src < NSRC; ++src)
 #pragma unroll
@@ -514,22 +540,47 @@ inline int env_int(const char *name, int dflt) {
 
 inline int mb_for(int M) { return M <= 4 ? 1 : (M <= 8 ? 2 : (M <= 16 ? 4 : 8)); }
 
+// Bytes of one staged group (A operands, scalars, zero table row).
+template <int FMT, int NSRC, int MB, int SPU>
+inline size_t unit_bytes(const Params &p) {
+    return (size_t)SPU * MB * 4 * p.rb * 16 + (size_t)p.M * 12 + (FMT == FMT_I8 ? 0 : (size_t)NSRC * 16);
+}
+
+template <int FMT, int NSRC, int XM, int MB, int SPU, bool PERM, bool COOP>
+int launch_kernel(st_context *ctx, Params &p, size_t lds) {
+    auto kern = qmv_kernel<FMT, NSRC, XM, MB, SPU, PERM, COOP>;
+    if (lds > 64 * 1024)
+        ST_HIP(hipFuncSetAttribute((const void *)kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds));
+    hipLaunchKernelGGL(kern, dim3(p.ntiles), dim3(64 * p.nwaves), lds, ctx->stream, p);
+    return launch_check("qmv_kernel");
+}
+
+constexpr size_t kCoopLdsBudget = 96 * 1024;
+
 template <int FMT, int NSRC, int XM, int MB, int SPU, bool PERM>
 int launch_t(st_context *ctx, Params &p) {
     constexpr int IPU = 4 * SPU;
     p.rb = p.M >= 4 ? 16 : 4 * p.M;
     p.chunk = std::max(1, 64 / (p.M * IPU));
     // Waves per workgroup: aim at ~4 waves per SIMD over the whole grid
-    // (each workgroup is one 16-column tile), and at most one chunk of
-    // groups per wave where that is possible.
-    int nw = 4;
-    if (kWide<FMT, NSRC, MB>) {
-        const int want = (ctx->num_cus * 16) / std::max(1, p.ntiles);
-        nw = want >= 16 ? 16 : (want >= 8 ? 8 : 4);
-        while (nw < kMaxWaves && (p.units + nw - 1) / nw > p.chunk) nw *= 2;
-        nw = std::min(nw, std::max(4, p.units));
-        nw = std::max(4, std::min(kMaxWaves, env_int("ST_QMV_WAVES", nw)));
+    // (each workgroup is one 16-column tile).
+    const int want = (ctx->num_cus * 16) / std::max(1, p.ntiles);
+    if constexpr (MB == 1 && FMT != FMT_I4) {
+        constexpr int NWX = kMaxWavesFor<NSRC, true>;
+        int nw = want >= 16 ? 16 : (want >= 8 ? 8 : 4);
+        nw = std::max(4, std::min({nw, NWX, std::max(4, p.units)}));
+        nw = std::max(4, std::min(NWX, env_int("ST_QMV_WAVES", nw)));
+        const size_t ub = unit_bytes<FMT, NSRC, MB, SPU>(p);
+        const size_t lds = ((ub * p.units + 15) & ~size_t(15)) + (size_t)nw * NSRC * MB * 64 * sizeof(float);
+        const long long items = (long long)p.M * p.units * IPU;
+        if (lds <= kCoopLdsBudget && items <= (long long)kCoopRounds * 64 * nw && !env_int("ST_QMV_NO_COOP", 0)) {
+            p.nwaves = nw;
+            p.wave_lds = (int)((ub * p.units + 15) & ~size_t(15));
+            return launch_kernel<FMT, NSRC, XM, MB, SPU, PERM, true>(ctx, p, lds);
+        }
     }
+    // fallback: per-wave chunked staging, 4 waves
+    const int nw = 4;
     p.nwaves = nw;
     const int max_units = (p.units + nw - 1) / nw;
     if (FMT != FMT_I8 && max_units > kMaxZeroUnits && (p.qz[0] || p.qz[1]))
@@ -538,11 +589,7 @@ int launch_t(st_context *ctx, Params &p) {
     const int ztab = (FMT == FMT_I8) ? 0 : std::min(max_units, kMaxZeroUnits) * NSRC * 16;
     p.wave_lds = (afr * 16 + p.chunk * p.M * 12 + ztab + 15) & ~15;
     const size_t lds = (size_t)nw * p.wave_lds + (size_t)nw * NSRC * MB * 64 * sizeof(float);
-    auto kern = qmv_kernel<FMT, NSRC, XM, MB, SPU, PERM>;
-    if (lds > 64 * 1024)
-        ST_HIP(hipFuncSetAttribute((const void *)kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds));
-    hipLaunchKernelGGL(kern, dim3(p.ntiles), dim3(64 * nw), lds, ctx->stream, p);
-    return launch_check("qmv_kernel");
+    return launch_kernel<FMT, NSRC, XM, MB, SPU, PERM, false>(ctx, p, lds);
 }
 
 template <int FMT, int NSRC, int XM, int SPU, bool PERM>

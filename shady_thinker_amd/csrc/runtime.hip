@@ -76,11 +76,12 @@ int st_context_set_stream(st_context *ctx, void *hip_stream) {
     if (!ctx) return st::fail(ST_ERR_INVALID, "st_context_set_stream: ctx is NULL");
     hipStream_t ns = static_cast<hipStream_t>(hip_stream);
     if (ns == ctx->stream) return ST_OK;
-    ST_HIP(hipSetDevice(ctx->device));
-    // Work already queued on the old stream keeps its order relative to the
-    // new one: wait for it before switching.
-    ST_HIP(hipStreamSynchronize(ctx->stream));
+    // No synchronisation here (it would be illegal under stream capture):
+    // ordering between the old and the new stream is the caller's, as for
+    // any library handle's set-stream call.
     if (ctx->own_stream) {
+        ST_HIP(hipSetDevice(ctx->device));
+        ST_HIP(hipStreamSynchronize(ctx->stream));  // our private stream: drain it before destroying
         ST_HIP(hipStreamDestroy(ctx->stream));
         ctx->own_stream = false;
     }
