@@ -58,6 +58,7 @@ def make_gptq(torch, dev, K, N, gen, gpu=None):
 
 
 def time_loop(torch, fn, iters, warmup):
+    """Average ms per call of fn(i), launched eagerly from Python."""
     for i in range(warmup):
         fn(i)
     s = torch.cuda.current_stream()
@@ -69,6 +70,58 @@ def time_loop(torch, fn, iters, warmup):
     e1.record(s)
     torch.cuda.synchronize()
     return e0.elapsed_time(e1) / iters  # ms
+
+
+class Replayer:
+    """Steps fn(0..period-1) captured as one HIP graph (plus shorter tail
+    graphs on demand), so that timing sees GPU time, not Python launch cost.
+    Decode loops are launch-bound; a serving loop replays a captured graph
+    the same way. Step i uses weight copy i % period (cold-cache rotation)."""
+
+    def __init__(self, torch, fn, period):
+        self.torch, self.fn, self.period = torch, fn, period
+        self.stream = torch.cuda.Stream()
+        self.graphs = {}
+        with torch.cuda.stream(self.stream):
+            for i in range(period):
+                fn(i)  # warm: first-call set-up happens outside capture
+        torch.cuda.synchronize()
+        self._graph(period)
+
+    def _graph(self, n):
+        if n not in self.graphs:
+            torch = self.torch
+            g = torch.cuda.CUDAGraph()
+            with torch.cuda.stream(self.stream):
+                with torch.cuda.graph(g, stream=self.stream):
+                    for i in range(n):
+                        self.fn(i)
+            torch.cuda.synchronize()
+            self.graphs[n] = g
+        return self.graphs[n]
+
+    def _steps(self, n):
+        full, tail = divmod(n, self.period)
+        for _ in range(full):
+            self._graph(self.period).replay()
+        if tail:
+            self._graph(tail).replay()
+
+    def run(self, iters, warmup):
+        """`warmup` untimed steps, then exactly `iters` timed steps; returns
+        ms per step."""
+        torch = self.torch
+        if iters % self.period:
+            self._graph(iters % self.period)  # capture outside the timed region
+        with torch.cuda.stream(self.stream):
+            self._steps(warmup)
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            torch.cuda.synchronize()
+            e0.record(self.stream)
+            self._steps(iters)
+            e1.record(self.stream)
+            torch.cuda.synchronize()
+        return e0.elapsed_time(e1) / iters
 
 
 def cpu_baseline(seconds=10.0):
@@ -103,8 +156,8 @@ def cpu_baseline(seconds=10.0):
 
 def load_traffic():
     """HBM bytes per launch of the dominant kernel from committed rocprofv3
-    --pmc runs (profiles/gate_up_traffic.json), if measured."""
-    p = os.path.join(ROOT, "profiles", "gate_up_traffic.json")
+    --pmc runs (profiles/qmv_gate_up_llama7b_traffic.json), if measured."""
+    p = os.path.join(ROOT, "profiles", "qmv_gate_up_llama7b_traffic.json")
     if os.path.exists(p):
         with open(p) as f:
             return json.load(f).get("traffic_bytes_per_launch")
@@ -120,7 +173,9 @@ def main():
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-gemm", action="store_true")
-    ap.add_argument("--only", default="", help="profile helper: run only this kernel (q|gate_up|down|gemm)")
+    ap.add_argument("--copy-calibrate", action="store_true",
+                    help="profiling helper: 10 plain 64 MiB device copies (calibrates FETCH_SIZE / WRITE_SIZE)")
+    ap.add_argument("--only", default="", help="profiling helper: launch only this kernel, eagerly (q|gate_up|down)")
     args = ap.parse_args()
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:
@@ -129,6 +184,15 @@ def main():
         sys.exit(2)
 
     import torch
+
+    if args.copy_calibrate:
+        a = torch.ones(16 << 20, device="cuda")  # 64 MiB
+        b = torch.empty_like(a)
+        for _ in range(10):
+            b.copy_(a)
+        torch.cuda.synchronize()
+        print(json.dumps({"copy_calibrate_bytes": a.numel() * 4, "calls": 10}))
+        return
 
     import shady_thinker_amd as sta
     from shady_thinker_amd import model as Mdl
@@ -183,14 +247,15 @@ def main():
     if args.only:
         fn = {"q": k_q, "gate_up": k_gu, "down": k_dn}.get(args.only)
         if fn is not None:
-            time_loop(torch, fn, args.steps, args.warmup)
-            print(json.dumps({"only": args.only, "steps": args.steps}))
+            ms = time_loop(torch, fn, args.steps, args.warmup)  # eager: one dispatch per call (for counters)
+            print(json.dumps({"only": args.only, "steps": args.steps, "ms_eager": round(ms, 5)}))
             return
 
-    ms_step = time_loop(torch, step, args.steps, args.warmup)
-    ms_q = time_loop(torch, k_q, args.steps, args.warmup)
-    ms_gu = time_loop(torch, k_gu, args.steps, args.warmup)
-    ms_dn = time_loop(torch, k_dn, args.steps, args.warmup)
+    ms_step = Replayer(torch, step, copies).run(args.steps, args.warmup)
+    ms_q = Replayer(torch, k_q, copies).run(args.steps, args.warmup)
+    ms_gu = Replayer(torch, k_gu, copies).run(args.steps, args.warmup)
+    ms_dn = Replayer(torch, k_dn, copies).run(args.steps, args.warmup)
+    ms_eager = time_loop(torch, step, args.steps, args.warmup)
     value = step_bytes / (ms_step * 1e-3) / 1e9
     gu_gbs = b_gu / (ms_gu * 1e-3) / 1e9
 
@@ -213,6 +278,8 @@ def main():
             "batch": 1, "group_size": GS, "cold_cache_copies": copies,
             "step_bytes": step_bytes, "hbm_frac": round(value / HBM_PEAK_GBS, 4),
         },
+        "ms_per_step_eager_python": round(ms_eager, 5),
+        "timing": "HIP-graph replay (one graph = one step per weight copy); events on the replay stream",
         "kernels": {
             "q_proj": {"ms": round(ms_q, 5), "bytes": b_q, "GB/s": round(b_q / ms_q / 1e6, 1)},
             "gate_up": {"ms": round(ms_gu, 5), "bytes": b_gu, "GB/s": round(gu_gbs, 1)},
@@ -247,7 +314,7 @@ def bench_gemm(torch, dev, gpu, Mdl, gen, args):
     except sta.ShadyHipError as e:
         return {"status": "not available", "error": str(e)}
     iters = max(5, min(50, args.steps // 4))
-    ms = time_loop(torch, lambda i: Mdl.gptq_gemm(gpu, A, qw, sc, C, K, N, GS, None, perm), iters, 3)
+    ms = Replayer(torch, lambda i: Mdl.gptq_gemm(gpu, A, qw, sc, C, K, N, GS, None, perm), 1).run(iters, 3)
     tf = 2.0 * Mr * K * N / (ms * 1e-3) / 1e12
     return {"M": Mr, "K": K, "N": N, "act_order": True, "ms": round(ms, 4), "TFLOP/s": round(tf, 1),
             "mfma_frac": round(tf / F16_MFMA_PEAK_TFLOPS, 4), "peak_TFLOP/s": F16_MFMA_PEAK_TFLOPS}

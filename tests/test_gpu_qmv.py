@@ -326,3 +326,41 @@ def test_repack_layout(gpu, orc):
                     pr = g * gs // 8 + 8 * (j // 2) + 2 * (lane // 16) + (j % 2)
                     exp[((t * G + g) * 64 + lane) * wpl + j] = c["qweight"][pr, min(16 * t + lane % 16, N - 1)]
     assert np.array_equal(got, exp)
+
+
+def test_graph_replay_matches_eager(gpu, orc):
+    """Captured decode kernels replayed several times, with eager work and
+    syncs in between, give the eager result every time (no state carried
+    between launches)."""
+    K, N = 4096, 1024
+    c = orc.gptq_case(95, K, N, 128)
+    w = up(gpu, c)
+    cu = orc.gptq_case(96, K, N, 128)
+    wu = up(gpu, cu)
+    x = torch.from_numpy(c["x"]).cuda()
+    y_eager = torch.empty(1, N, device="cuda")
+    y2_eager = torch.empty(1, N, device="cuda")
+    M.gptq_matvec(gpu, "t", x, w.qweight, w.scales, y_eager, K, N, 128, flags=w.flags)
+    M.fused_gate_up_silu(gpu, x, w.qweight, w.scales, wu.qweight, wu.scales, y2_eager, K, N, 128, flags=w.flags)
+    torch.cuda.synchronize()
+    s = torch.cuda.Stream()
+    y = torch.zeros(1, N, device="cuda")
+    y2 = torch.zeros(1, N, device="cuda")
+    with torch.cuda.stream(s):
+        M.gptq_matvec(gpu, "t", x, w.qweight, w.scales, y, K, N, 128, flags=w.flags)  # warm on s
+        torch.cuda.synchronize()
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g, stream=s):
+            M.gptq_matvec(gpu, "t", x, w.qweight, w.scales, y, K, N, 128, flags=w.flags)
+            M.fused_gate_up_silu(gpu, x, w.qweight, w.scales, wu.qweight, wu.scales, y2, K, N, 128, flags=w.flags)
+    for rep in range(4):
+        y.fill_(float("nan"))
+        y2.fill_(float("nan"))
+        torch.cuda.synchronize()
+        with torch.cuda.stream(s):
+            g.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(y, y_eager), rep
+        assert torch.equal(y2, y2_eager), rep
+        M.gptq_matvec(gpu, "t", x, w.qweight, w.scales, y_eager, K, N, 128, flags=w.flags)  # eager work between
+        torch.cuda.synchronize()
