@@ -1,0 +1,154 @@
+"""GPU parity of the prefill GEMM st_gptq_i4_gemm against the CPU oracle and
+a torch fp32 reference, through the C ABI.
+
+Bar: GEMM outputs within rel-L2 2e-3. The kernel
+keeps the dequant exact ((q - z) as f16 integers, the f16 scale applied to
+each group's f32 partial), so with f32 output it sits far below the bar;
+one-hot rows and integer-valued cases are checked bit for bit.
+"""
+import numpy as np
+import pytest
+import torch
+
+import shady_thinker_amd as sta
+from shady_thinker_amd import model as M
+
+pytestmark = pytest.mark.gpu
+
+TOL = 2e-3  # rel-L2, prefill GEMM (north_star)
+
+
+def up(gpu, case, zeros_plus_one=False, tiled=True):
+    return sta.GptqWeight.upload(gpu, case["qweight"], case["scales"], case["gs"], qzeros=case["qzeros"],
+                                 g_idx=case["g_idx"], zeros_plus_one=zeros_plus_one, tiled=tiled)
+
+
+def run_gemm(gpu, w, a_np, out_dtype=torch.float32):
+    a = torch.from_numpy(np.ascontiguousarray(a_np, dtype=np.float16)).to(gpu.device)
+    c = torch.empty(a.shape[0], w.N, dtype=out_dtype, device=gpu.device)
+    M.gptq_gemm(gpu, a, w.qweight, w.scales, c, w.K, w.N, w.group_size, w.qzeros, w.perm, w.flags)
+    torch.cuda.synchronize()
+    return c.float().cpu().numpy()
+
+
+@pytest.mark.parametrize("tiled", [True, False])
+@pytest.mark.parametrize("Mr,K,N,gs,zeros,act", [
+    (1, 256, 64, 128, False, False),
+    (33, 512, 200, 128, False, False),
+    (130, 1024, 264, 64, True, False),
+    (257, 2048, 520, 256, False, True),
+    (96, 1024, 136, 128, True, True),
+    (129, 768, 384, 64, False, True),
+])
+def test_gemm_matches_oracle(gpu, orc, tiled, Mr, K, N, gs, zeros, act):
+    c = orc.gptq_case(10 + Mr, K, N, gs, zeros=zeros, act_order=act, M=Mr, x_dtype=np.float16)
+    w = up(gpu, c, tiled=tiled)
+    y = run_gemm(gpu, w, c["x"])
+    ref = orc.gptq_matvec_f64(c["x"], c["qweight"], c["scales"], K, N, gs, qzeros=c["qzeros"], g_idx=c["g_idx"])
+    e = orc.rel_l2(y, ref)
+    print(f"gemm M={Mr} K={K} N={N} gs={gs} zeros={zeros} act={act} tiled={tiled}: rel-L2 {e:.3e}")
+    assert e < TOL
+    assert e < 1e-5  # exact dequant + f32 accumulation: far below the bar
+
+
+@pytest.mark.parametrize("tiled", [True, False])
+def test_gemm_f16_output_and_zeros_plus_one(gpu, orc, tiled):
+    Mr, K, N, gs = 200, 1024, 328, 128
+    c = orc.gptq_case(5, K, N, gs, zeros=True, M=Mr, x_dtype=np.float16)
+    w = up(gpu, c, zeros_plus_one=True, tiled=tiled)
+    y = run_gemm(gpu, w, c["x"], torch.float16)
+    ref = orc.gptq_matvec_f64(c["x"], c["qweight"], c["scales"], K, N, gs, qzeros=c["qzeros"], zero_offset=1)
+    e = orc.rel_l2(y, ref)
+    print(f"gemm f16 out, zeros+1: rel-L2 {e:.3e}")
+    assert e < TOL
+
+
+@pytest.mark.parametrize("tiled", [True, False])
+def test_gemm_one_hot_rows_are_dequant_rows(gpu, orc, tiled):
+    K, N, gs = 1024, 264, 128
+    c = orc.gptq_case(1, K, N, gs, zeros=True)
+    w = up(gpu, c, tiled=tiled)
+    W = orc.gptq_dequant_f32(c["qweight"], c["scales"], K, N, gs, qzeros=c["qzeros"])
+    ks = [0, 1, 7, 8, 63, 64, 127, 128, 500, 1023] * 4  # 40 rows: more than one MFMA block
+    a = np.zeros((len(ks), K), np.float16)
+    for i, k in enumerate(ks):
+        a[i, k] = 1.0
+    y = run_gemm(gpu, w, a)
+    assert np.array_equal(y, W[ks]), "dequantized rows must be bit-exact"
+
+
+def test_gemm_integer_case_bit_equal(gpu, orc):
+    Mr, K, N, gs = 64, 2048, 256, 128
+    c = orc.gptq_case(2, K, N, gs, zeros=True, act_order=True)
+    c["scales"] = np.ones_like(c["scales"])
+    rng = np.random.default_rng(3)
+    a = rng.integers(-3, 4, size=(Mr, K)).astype(np.float16)
+    w = up(gpu, c)
+    y = run_gemm(gpu, w, a)
+    ref = orc.gptq_matvec_f64(a, c["qweight"], c["scales"], K, N, gs, qzeros=c["qzeros"], g_idx=c["g_idx"])
+    assert np.array_equal(y.astype(np.float64), ref)
+
+
+def test_gemm_agrees_with_decode_on_shared_rows(gpu, orc):
+    """linear() sends M <= 32 to the matvec and M > 32 to the GEMM; the two
+    must agree on the same weights (both are exact-dequant, f32-accumulate)."""
+    K, N, gs = 2048, 512, 128
+    c = orc.gptq_case(4, K, N, gs, act_order=True, M=48, x_dtype=np.float16)
+    w = up(gpu, c)
+    x = torch.from_numpy(c["x"]).to(gpu.device)
+    y_g = torch.empty(48, N, device=gpu.device)
+    sta.linear(gpu, x, w, y_g)
+    y_m = torch.empty(16, N, device=gpu.device)
+    sta.linear(gpu, x[:16].contiguous(), w, y_m)
+    torch.cuda.synchronize()
+    e = orc.rel_l2(y_g[:16].cpu().numpy(), y_m.cpu().numpy())
+    assert e < 1e-5
+
+
+def test_gemm_full_config_vs_torch_fp32(gpu, orc):
+    """configs[3] at full size (M=2048, K=4096, N=14336, act-order): torch
+    fp32 matmul over the exact f32 dequant (st_gptq_i4_dequant)."""
+    Mr, K, N, gs = 2048, 4096, 14336, 128
+    g = torch.Generator(device=gpu.device)
+    g.manual_seed(7)
+    qw = torch.randint(-2 ** 31, 2 ** 31 - 1, (K // 8, N), generator=g, device=gpu.device, dtype=torch.int32)
+    sc = (torch.rand(K // gs, N, generator=g, device=gpu.device) * 0.02 + 1e-3).half()
+    perm = torch.randperm(K, generator=g, device=gpu.device).to(torch.int32)
+    A = torch.randn(Mr, K, generator=g, device=gpu.device).half()
+    C = torch.empty(Mr, N, device=gpu.device, dtype=torch.float32)
+    M.gptq_gemm(gpu, A, qw, sc, C, K, N, gs, None, perm)
+    W = torch.empty(K, N, device=gpu.device, dtype=torch.float32)
+    M.gptq_dequant(gpu, qw, sc, W, K, N, gs)  # rows in stored (sorted) order
+    ref = A[:, perm.long()].float() @ W
+    torch.cuda.synchronize()
+    e = (torch.linalg.vector_norm((C - ref).double()) / torch.linalg.vector_norm(ref.double())).item()
+    print(f"configs[3] gemm vs torch fp32: rel-L2 {e:.3e}")
+    assert e < TOL
+    assert e < 1e-5
+
+
+def test_gemm_graph_replay_matches_eager(gpu, orc):
+    Mr, K, N, gs = 160, 1024, 392, 128
+    c = orc.gptq_case(8, K, N, gs, act_order=True, M=Mr, x_dtype=np.float16)
+    w = up(gpu, c)
+    a = torch.from_numpy(c["x"]).to(gpu.device)
+    eager = torch.empty(Mr, N, device=gpu.device)
+    M.gptq_gemm(gpu, a, w.qweight, w.scales, eager, K, N, gs, w.qzeros, w.perm, w.flags)
+    torch.cuda.synchronize()
+    out = torch.empty_like(eager)
+    s = torch.cuda.Stream()
+    with torch.cuda.stream(s):
+        M.gptq_gemm(gpu, a, w.qweight, w.scales, out, K, N, gs, w.qzeros, w.perm, w.flags)  # warm on s
+        torch.cuda.synchronize()
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph, stream=s):
+            M.gptq_gemm(gpu, a, w.qweight, w.scales, out, K, N, gs, w.qzeros, w.perm, w.flags)
+    for i in range(3):
+        out.fill_(float("nan"))
+        torch.cuda.synchronize()
+        with torch.cuda.stream(s):
+            graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out, eager), f"replay {i}"
+        M.gptq_gemm(gpu, a, w.qweight, w.scales, eager, K, N, gs, w.qzeros, w.perm, w.flags)  # eager work between
+        torch.cuda.synchronize()
