@@ -6,23 +6,33 @@
 //  * B operand = (q - z) as integer-valued f16 (exact: |q - z| <= 15). A
 //    GPTQ word holds 8 consecutive k of one column, which is exactly one
 //    lane's B fragment of v_mfma_f32_32x32x16_f16, so weights go straight
-//    from HBM to registers (no LDS): word -> 4 f16 pairs with one shift,
-//    one and-or with the f16 1024 bias, one packed subtract each.
+//    from HBM to registers (no LDS). Word -> 4 f16 pairs in 9 VALU ops:
+//    and-or of the even nibble pairs into the f16 1024 bias (1024 + q),
+//    of the odd pairs in place (1024 + 16 q), one shift by 8 for the upper
+//    half; then one packed subtract (- (1024 + z)) or one packed fma
+//    (* 1/16 - (64 + z)) per pair. Every step is exact in f16.
 //  * Each group (128 k) accumulates in f32 from zero; its partial is then
 //    multiplied by the column's f16 scale and added to the running total.
 //    So the only roundings are the MFMA's f32 accumulation and one f32
 //    multiply-add per group, as in an f32 dequant-then-GEMM.
-//  * A (activations, f16) is staged through LDS, double buffered, with a
-//    padded row stride; each lane's 8 halves are stored in the order of the
-//    B register halves (k = 0,4,1,5,2,6,3,7 within the 8), so A and B
-//    fragments pair element for element.
-//  * Workgroup tile 128 (M) x 128 (N), 4 waves as 2 x 2, each wave 64 x 64 =
-//    2 x 2 MFMA blocks of 32 x 32 (group partials + totals: 128 registers,
-//    so two waves fit per SIMD). Tiles are ordered XCD-major: the workgroups of
-//    one XCD share A rows, which then stay in that XCD's L2.
+//  * A (activations, f16) first goes through a pre-pass (prep_a_kernel)
+//    into the context workspace: act-order column gather if any, and each
+//    8-k chunk reordered to the B register order (k = 0,4,1,5,2,6,3,7), so A
+//    and B fragments pair element for element. The GEMM then moves A tiles
+//    HBM -> LDS with the buffer-to-LDS DMA (no registers, no VALU), double
+//    buffered one tile ahead. A DMA instruction fills 1 KiB of LDS lane by
+//    lane, so rows are not padded: row r's 16-byte chunk c sits at chunk
+//    c ^ (r % 16), which makes the MFMA fragment reads conflict-free.
+//  * Workgroup tile 128 (M) x 256 (N), 4 waves side by side along N, each
+//    wave 128 x 64 = 4 x 2 MFMA blocks of 32 x 32: every converted B
+//    fragment feeds 4 MFMAs, every A fragment read from LDS feeds 2, and no
+//    B column is converted twice in a workgroup. Group partials + totals take
+//    256 registers: one wave per SIMD, latency hidden by the one-tile-ahead
+//    prefetch of A (registers -> LDS) and B (registers). Tiles are ordered
+//    XCD-major: the workgroups of one XCD share A rows, which then stay in
+//    that XCD's L2.
 //  * Act-order: K is sorted by group at upload (st_gptq_i4_act_order); the
-//    matching column gather of A runs first (permute_cols_kernel) into the
-//    context workspace.
+//    matching column gather of A is part of the pre-pass.
 #include "common.hpp"
 
 #include <algorithm>
@@ -37,46 +47,61 @@ typedef unsigned u32x4 __attribute__((ext_vector_type(4)));
 typedef unsigned u32x2 __attribute__((ext_vector_type(2)));
 
 constexpr int BM = 128;              // rows of A per workgroup
-constexpr int BN = 128;              // columns per workgroup
-constexpr int WN = 2;                // waves along N (and 2 along M)
-constexpr int RB = 2, CB = 2;        // 32 x 32 MFMA blocks per wave (rows, columns)
+constexpr int BN = 256;              // columns per workgroup
+constexpr int WN = 4;                // waves along N (1 along M)
+constexpr int RB = 4, CB = 2;        // 32 x 32 MFMA blocks per wave (rows, columns)
 constexpr int KT = 128;              // k per LDS tile
-constexpr int ALD = KT + 8;          // LDS row stride in halves (padding against bank conflicts)
 constexpr int kThreads = 256;
+#ifndef ST_GEMM_WAVES
+#define ST_GEMM_WAVES 2
+#endif
+constexpr int kWavesPerSimd = ST_GEMM_WAVES;
 // Buffer resource word 3 for gfx9-class GPUs: raw (untyped) 32-bit data.
 constexpr int kRsrcWord3 = 0x00020000;
-constexpr int kChunks = BM * KT / 8 / kThreads;  // 16-byte A chunks per thread per tile (8)
+constexpr int kDmaPerWave = BM * KT * 2 / 1024 / (kThreads / 64);  // 1 KiB A DMAs per wave per tile (8)
 
-// 8 halves k..k+7 (4 dwords a0..a3 = (k0,k1),(k2,k3),(k4,k5),(k6,k7)) ->
-// register order of the B conversion: (k0,k4),(k1,k5),(k2,k6),(k3,k7).
-__device__ __forceinline__ u32x4 to_b_order(u32x4 a) {
-    u32x4 r;
-    r.x = __builtin_amdgcn_perm(a.z, a.x, 0x05040100u);  // lo(a.x), lo(a.z)
-    r.y = __builtin_amdgcn_perm(a.z, a.x, 0x07060302u);  // hi(a.x), hi(a.z)
-    r.z = __builtin_amdgcn_perm(a.w, a.y, 0x05040100u);  // lo(a.y), lo(a.w)
-    r.w = __builtin_amdgcn_perm(a.w, a.y, 0x07060302u);  // hi(a.y), hi(a.w)
+// v_and_or_b32 with both constants in VGPRs (a VOP3 on gfx9 takes no
+// literal, and at most one SGPR), so the compiler cannot split it in two.
+__device__ __forceinline__ unsigned and_or(unsigned a, unsigned m, unsigned c) {
+    unsigned r;
+    asm("v_and_or_b32 %0, %1, %2, %3" : "=v"(r) : "v"(a), "v"(m), "v"(c));
     return r;
 }
 
+struct BConv {
+    unsigned m_lo, m_hi, bias;  // 0x000F000F, 0x00F000F0, f16 1024 in both halves
+    half2_t zlo;                // 1024 + z
+    half2_t zhi;                // -(64 + z)
+    half2_t sh;                 // the group's scale
+};
+
 // GPTQ word (nibbles n0..n7 = k0..k7) -> B fragment halves
-// (n0,n4),(n1,n5),(n2,n6),(n3,n7) minus the zero point, exact.
-__device__ __forceinline__ half8 word_to_b(unsigned w, half2_t zb) {
-    half8 b;
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-        const unsigned t = ((w >> (4 * j)) & 0x000F000Fu) | 0x64006400u;  // f16 1024 + n
-        const half2_t h = __builtin_bit_cast(half2_t, t) - zb;            // (n - z), exact
-        b[2 * j] = h.x;
-        b[2 * j + 1] = h.y;
-    }
-    return b;
+// (n0,n4),(n1,n5),(n2,n6),(n3,n7), each (q - z) * s: (q - z) is formed
+// exactly (1024 + q - (1024 + z), or (1024 + 16 q) / 16 - (64 + z)), then
+// one f16 multiply by the group scale rounds it once.
+__device__ __forceinline__ half8 word_to_b(unsigned w, const BConv &c) {
+    const half2_t sixteenth = {(_Float16)0.0625f, (_Float16)0.0625f};
+    const unsigned w8 = w >> 8;
+    const half2_t h0 = (__builtin_bit_cast(half2_t, and_or(w, c.m_lo, c.bias)) - c.zlo) * c.sh;
+    const half2_t h1 =
+        __builtin_elementwise_fma(__builtin_bit_cast(half2_t, and_or(w, c.m_hi, c.bias)), sixteenth, c.zhi) * c.sh;
+    const half2_t h2 = (__builtin_bit_cast(half2_t, and_or(w8, c.m_lo, c.bias)) - c.zlo) * c.sh;
+    const half2_t h3 =
+        __builtin_elementwise_fma(__builtin_bit_cast(half2_t, and_or(w8, c.m_hi, c.bias)), sixteenth, c.zhi) * c.sh;
+    const u32x4 r = {__builtin_bit_cast(unsigned, h0), __builtin_bit_cast(unsigned, h1), __builtin_bit_cast(unsigned, h2),
+                     __builtin_bit_cast(unsigned, h3)};
+    return __builtin_bit_cast(half8, r);
 }
 
 template <int GS, bool TILED, bool F16OUT>
-__global__ __launch_bounds__(kThreads, (GS == 64 ? 1 : 2)) void gemm_kernel(const _Float16 *__restrict__ A, const uint32_t *__restrict__ qw,
+__global__ __launch_bounds__(kThreads, kWavesPerSimd) void gemm_kernel(const _Float16 *__restrict__ A, const uint32_t *__restrict__ qw,
                                                            const uint16_t *__restrict__ sc, const uint32_t *__restrict__ qz,
                                                            int zoff, void *__restrict__ C, int M, int K, int N) {
-    __shared__ __align__(16) _Float16 As[2][BM * ALD];
+    // Two separate arrays (not one [2][...]) so that alias analysis can tell
+    // the stage being read from the stage the DMA is filling; otherwise every
+    // LDS read waits for the in-flight DMA.
+    __shared__ __align__(16) _Float16 As0[BM * KT];
+    __shared__ __align__(16) _Float16 As1[BM * KT];
 
     const int tid = threadIdx.x;
     const int lane = tid & 63;
@@ -106,12 +131,21 @@ __global__ __launch_bounds__(kThreads, (GS == 64 ? 1 : 2)) void gemm_kernel(cons
     // the 24 loads per tile need no 64-bit address registers.
     const __amdgpu_buffer_rsrc_t ra = __builtin_amdgcn_make_buffer_rsrc((void *)A, (short)0, 0x7FFFFFFF, kRsrcWord3);
     const __amdgpu_buffer_rsrc_t rb_ = __builtin_amdgcn_make_buffer_rsrc((void *)qw, (short)0, 0x7FFFFFFF, kRsrcWord3);
-    int aoff[kChunks];  // bytes: row (clamped to M - 1) and 16-byte chunk of this thread's A loads
+    // A DMA j of this wave fills tile rows 4 (8 wave + j) .. +3; lane i
+    // writes LDS chunk i % 16 of row + i / 16, i.e. logical chunk
+    // (i % 16) ^ (row % 16). Rows past M - 1 repeat row M - 1.
+    auto a_dma = [&](auto STAGE, int kt) {
+        _Float16 *as = decltype(STAGE)::value ? As1 : As0;
 #pragma unroll
-    for (int j = 0; j < kChunks; ++j) {
-        const int c = tid + kThreads * j;
-        aoff[j] = (min(m0 + (c >> 4), M - 1) * K + 8 * (c & 15)) * 2;
-    }
+        for (int j = 0; j < kDmaPerWave; ++j) {
+            const int r = 4 * (kDmaPerWave * wave + j) + (lane >> 4);
+            const int c = (lane & 15) ^ (r & 15);
+            const int voff = (min(m0 + r, M - 1) * K + 8 * c) * 2;
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(
+                ra, (__attribute__((address_space(3))) void *)&as[(4 * (kDmaPerWave * wave + j)) * KT], 16, voff,
+                kt * KT * 2, 0, 0);
+        }
+    };
     // B words: bw[buffer][t][cb] is the word of k-step t (16 k) for this
     // lane's column block cb; koff(t) is where its 8 k sit in the A tile.
     //  * [K/8, N] layout: k-step t, lane half hi -> packed row 2t + hi.
@@ -133,20 +167,9 @@ __global__ __launch_bounds__(kThreads, (GS == 64 ? 1 : 2)) void gemm_kernel(cons
             boff[cb] = (hi * N + col[cb]) * 4;
         }
     }
-    auto koff = [&](int t) { return TILED ? 64 * (t >> 2) + 32 * hi + 16 * ((t >> 1) & 1) + 8 * (t & 1) : 16 * t + 8 * hi; };
+    // logical 16-byte chunk (8 k) of the A tile that k-step t uses in this lane
+    auto kchunk = [&](int t) { return TILED ? 8 * (t >> 2) + 4 * hi + 2 * ((t >> 1) & 1) + (t & 1) : 2 * t + hi; };
 
-    u32x4 apre[kChunks];
-    auto load_a = [&](int kt) {
-#pragma unroll
-        for (int j = 0; j < kChunks; ++j) apre[j] = __builtin_amdgcn_raw_buffer_load_b128(ra, aoff[j], kt * KT * 2, 0);
-    };
-    auto store_a = [&](int buf) {
-#pragma unroll
-        for (int j = 0; j < kChunks; ++j) {
-            const int c = tid + kThreads * j;
-            *reinterpret_cast<u32x4 *>(&As[buf][(c >> 4) * ALD + 8 * (c & 15)]) = to_b_order(apre[j]);
-        }
-    };
     unsigned bw[2][KT / 16][CB];
     auto load_b = [&](unsigned (&dst)[KT / 16][CB], int kt) {
 #pragma unroll
@@ -176,84 +199,106 @@ __global__ __launch_bounds__(kThreads, (GS == 64 ? 1 : 2)) void gemm_kernel(cons
         }
     };
 
-    f32x16 acc[RB][CB], tot[RB][CB];
+    f32x16 acc[RB][CB];
 #pragma unroll
     for (int rb = 0; rb < RB; ++rb)
 #pragma unroll
-        for (int cb = 0; cb < CB; ++cb) {
-            acc[rb][cb] = f32x16{};
-            tot[rb][cb] = f32x16{};
-        }
+        for (int cb = 0; cb < CB; ++cb) acc[rb][cb] = f32x16{};
 
-    half2_t zb[CB];
-    float s[CB];
-    // zero point (as f16 1024 + z in both halves) and scale of group g
+    BConv bc[CB];
+#pragma unroll
+    for (int cb = 0; cb < CB; ++cb) {
+        bc[cb].m_lo = 0x000F000Fu;
+        bc[cb].m_hi = 0x00F000F0u;
+        bc[cb].bias = 0x64006400u;
+    }
+    // Group constants: the raw scale / zero words of a tile's groups are
+    // loaded one tile ahead, before that tile's A and B loads. Loads complete
+    // in issue order, so a scale load issued after the prefetch would make
+    // its wait drain the whole prefetch.
+    constexpr int GPT = KT / GS > 0 ? KT / GS : 1;  // groups starting per tile (GS = 256: one, every other tile)
     const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc((void *)sc, (short)0, 0x7FFFFFFF, kRsrcWord3);
+    // Without qzeros the zero words are read from the scales (always in
+    // bounds: G * N/8 words < G * N halves) and ignored, so the load needs no
+    // branch.
+    const bool has_z = qz != nullptr;
     const __amdgpu_buffer_rsrc_t rz =
-        __builtin_amdgcn_make_buffer_rsrc((void *)(qz ? qz : qw), (short)0, 0x7FFFFFFF, kRsrcWord3);
-    auto group_consts = [&](int g) {
+        __builtin_amdgcn_make_buffer_rsrc((void *)(has_z ? (const void *)qz : (const void *)sc), (short)0, 0x7FFFFFFF,
+                                          kRsrcWord3);
+    unsigned sraw[2][GPT][CB], zraw[2][GPT][CB];
+    auto load_groups = [&](int slot, int kt) {
+#pragma unroll
+        for (int gi = 0; gi < GPT; ++gi) {
+            const int g = (kt * KT) / GS + gi;
+#pragma unroll
+            for (int cb = 0; cb < CB; ++cb) {
+                sraw[slot][gi][cb] = __builtin_amdgcn_raw_buffer_load_b32(rs, (col[cb] >> 1) * 4, g * N * 2, 0);
+                zraw[slot][gi][cb] = __builtin_amdgcn_raw_buffer_load_b32(rz, (col[cb] >> 3) * 4, g * (N >> 3) * 4, 0);
+            }
+        }
+    };
+    auto group_consts = [&](int slot, int gi) {
 #pragma unroll
         for (int cb = 0; cb < CB; ++cb) {
-            int z = 8;
-            if (qz)
-                z = (int)((__builtin_amdgcn_raw_buffer_load_b32(rz, (col[cb] >> 3) * 4, g * (N >> 3) * 4, 0) >>
-                           (4 * (col[cb] & 7))) &
-                          0xF) +
-                    zoff;
-            const _Float16 zz = (_Float16)(1024 + z);
-            zb[cb] = half2_t{zz, zz};
-            const unsigned sw = __builtin_amdgcn_raw_buffer_load_b32(rs, (col[cb] >> 1) * 4, g * N * 2, 0);
-            s[cb] = (float)__builtin_bit_cast(_Float16, (uint16_t)(sw >> (16 * (col[cb] & 1))));
+            const int z = has_z ? (int)((zraw[slot][gi][cb] >> (4 * (col[cb] & 7))) & 0xF) + zoff : 8;
+            const _Float16 zl = (_Float16)(1024 + z), zh = (_Float16)(-(64 + z));
+            bc[cb].zlo = half2_t{zl, zl};
+            bc[cb].zhi = half2_t{zh, zh};
+            const _Float16 sf = __builtin_bit_cast(_Float16, (uint16_t)(sraw[slot][gi][cb] >> (16 * (col[cb] & 1))));
+            bc[cb].sh = half2_t{sf, sf};
         }
     };
 
-    load_a(0);
+    load_groups(0, 0);
+    a_dma(std::integral_constant<int, 0>{}, 0);
     load_b(bw[0], 0);
-    store_a(0);
+    __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): this wave's DMAs are in LDS
     __syncthreads();
 
     // One K tile from LDS buffer BUF = kt & 1. The tile loop is unrolled by
     // two so that the register buffer index and the group boundaries are
     // compile-time (kt * KT mod GS depends only on BUF for GS <= 2 KT).
+    // Software pipeline over the 8 k-steps: the A fragments (LDS) and the
+    // converted B of step t + 1 are produced while step t's MFMAs run.
     auto tile = [&](auto BUFC, int kt) {
         constexpr int BUF = decltype(BUFC)::value;
-        const bool more = kt + 1 < ntiles;
-        if (more) {
-            load_a(kt + 1);
-            load_b(bw[BUF ^ 1], kt + 1);
-        }
+        // The prefetch, its wait and the barrier are unconditional (the last
+        // tile reloads itself into the idle stage): with no branch around
+        // them, the compiler's wait counting never sees a path on which a
+        // previous tile's loads are still in flight.
+        const int kn = min(kt + 1, ntiles - 1);
+        load_groups(BUF ^ 1, kn);
+        a_dma(std::integral_constant<int, BUF ^ 1>{}, kn);  // stage BUF ^ 1 was last read before the previous barrier
+        load_b(bw[BUF ^ 1], kn);
+        half8 af[2][RB];
+        auto read_a = [&](int t, int slot) {
 #pragma unroll
-        for (int s16 = 0; s16 < KT / 16; ++s16) {
-            const int kin = BUF * KT + 16 * s16;  // == k mod GS (mod 2 KT)
-            if (kin % GS == 0) group_consts((kt * KT + 16 * s16) / GS);
+            for (int rb = 0; rb < RB; ++rb)
+            {
+                const int row = mw + rb * 32 + l32;
+                const _Float16 *as = BUF ? As1 : As0;
+                af[slot][rb] = *reinterpret_cast<const half8 *>(&as[row * KT + 8 * (kchunk(t) ^ (row & 15))]);
+            }
+        };
+        read_a(0, 0);
+#pragma unroll
+        for (int t = 0; t < KT / 16; ++t) {
+            const int cur = t & 1;
+            if (t + 1 < KT / 16) read_a(t + 1, cur ^ 1);
+            if ((BUF * KT + 16 * t) % GS == 0) group_consts(BUF, (16 * t) / GS);
             half8 bf[CB];
 #pragma unroll
-            for (int cb = 0; cb < CB; ++cb) bf[cb] = word_to_b(bw[BUF][s16][cb], zb[cb]);
+            for (int cb = 0; cb < CB; ++cb) bf[cb] = word_to_b(bw[BUF][t][cb], bc[cb]);
 #pragma unroll
-            for (int rb = 0; rb < RB; ++rb) {
-                const half8 af =
-                    *reinterpret_cast<const half8 *>(&As[BUF][(mw + rb * 32 + l32) * ALD + koff(s16)]);
+            for (int rb = 0; rb < RB; ++rb)
 #pragma unroll
                 for (int cb = 0; cb < CB; ++cb)
-                    acc[rb][cb] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af, bf[cb], acc[rb][cb], 0, 0, 0);
-            }
-            if ((kin + 16) % GS == 0) {  // group complete: scale into the total
-#pragma unroll
-                for (int rb = 0; rb < RB; ++rb)
-#pragma unroll
-                    for (int cb = 0; cb < CB; ++cb) {
-#pragma unroll
-                        for (int i = 0; i < 16; ++i) tot[rb][cb][i] = fmaf(acc[rb][cb][i], s[cb], tot[rb][cb][i]);
-                        acc[rb][cb] = f32x16{};
-                    }
-            }
+                    acc[rb][cb] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af[cur][rb], bf[cb], acc[rb][cb], 0, 0, 0);
         }
-        if (more) {
-            store_a(BUF ^ 1);
-            __syncthreads();
-        }
+        __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): next tile's A DMAs (and B words) landed
+        __syncthreads();
     };
-    // K % 256 == 0 when GS == 256, so its groups never end on an odd last tile.
+    // K % 256 == 0 when GS == 256, so a group never ends on an odd last tile.
     for (int kt = 0; kt < ntiles; kt += 2) {
         tile(std::integral_constant<int, 0>{}, kt);
         if (kt + 1 < ntiles) tile(std::integral_constant<int, 1>{}, kt + 1);
@@ -272,22 +317,50 @@ __global__ __launch_bounds__(kThreads, (GS == 64 ? 1 : 2)) void gemm_kernel(cons
                 const int m = m0 + mw + rb * 32 + 8 * (i >> 2) + 4 * hi + (i & 3);
                 if (m >= M) continue;
                 if constexpr (F16OUT)
-                    static_cast<_Float16 *>(C)[(size_t)m * N + n] = (_Float16)tot[rb][cb][i];
+                    static_cast<_Float16 *>(C)[(size_t)m * N + n] = (_Float16)acc[rb][cb][i];
                 else
-                    static_cast<float *>(C)[(size_t)m * N + n] = tot[rb][cb][i];
+                    static_cast<float *>(C)[(size_t)m * N + n] = acc[rb][cb][i];
             }
         }
 }
 
-// A'[m][j] = A[m][perm[j]]: one workgroup per row, the row staged in LDS.
-__global__ __launch_bounds__(256) void permute_cols_kernel(const _Float16 *__restrict__ A, const int32_t *__restrict__ perm,
-                                                           _Float16 *__restrict__ out, int K) {
+// 8 halves k..k+7 (4 dwords a0..a3 = (k0,k1),(k2,k3),(k4,k5),(k6,k7)) ->
+// register order of the B conversion: (k0,k4),(k1,k5),(k2,k6),(k3,k7).
+__device__ __forceinline__ u32x4 to_b_order(u32x4 a) {
+    u32x4 r;
+    r.x = __builtin_amdgcn_perm(a.z, a.x, 0x05040100u);  // lo(a.x), lo(a.z)
+    r.y = __builtin_amdgcn_perm(a.z, a.x, 0x07060302u);  // hi(a.x), hi(a.z)
+    r.z = __builtin_amdgcn_perm(a.w, a.y, 0x05040100u);  // lo(a.y), lo(a.w)
+    r.w = __builtin_amdgcn_perm(a.w, a.y, 0x07060302u);  // hi(a.y), hi(a.w)
+    return r;
+}
+
+// GEMM A operand: A'[m][8c + i] = A[m][perm[8c + o(i)]] (perm = identity
+// when NULL), o = (0,4,1,5,2,6,3,7): the act-order gather and the B
+// register order of each 8-k chunk in one pass. One workgroup per row, the
+// row staged in LDS.
+__global__ __launch_bounds__(256) void prep_a_kernel(const _Float16 *__restrict__ A, const int32_t *__restrict__ perm,
+                                                     _Float16 *__restrict__ out, int K) {
     extern __shared__ _Float16 row[];
     const size_t base = (size_t)blockIdx.x * K;
     for (int k = threadIdx.x * 8; k < K; k += 256 * 8)
         *reinterpret_cast<u32x4 *>(&row[k]) = *reinterpret_cast<const u32x4 *>(A + base + k);
     __syncthreads();
-    for (int j = threadIdx.x; j < K; j += 256) out[base + j] = row[perm[j]];
+    for (int k = threadIdx.x * 8; k < K; k += 256 * 8) {
+        u32x4 v;
+        if (perm) {
+            const u32x4 p0 = *reinterpret_cast<const u32x4 *>(perm + k);
+            const u32x4 p1 = *reinterpret_cast<const u32x4 *>(perm + k + 4);
+            const unsigned short *rs = reinterpret_cast<const unsigned short *>(row);
+            v.x = rs[p0.x] | ((unsigned)rs[p1.x] << 16);
+            v.y = rs[p0.y] | ((unsigned)rs[p1.y] << 16);
+            v.z = rs[p0.z] | ((unsigned)rs[p1.z] << 16);
+            v.w = rs[p0.w] | ((unsigned)rs[p1.w] << 16);
+        } else {
+            v = to_b_order(*reinterpret_cast<const u32x4 *>(&row[k]));
+        }
+        *reinterpret_cast<u32x4 *>(out + base + k) = v;
+    }
 }
 
 template <int GS, bool TILED>
@@ -329,19 +402,16 @@ extern "C" int st_gptq_i4_gemm(st_context *ctx, const uint16_t *a, const uint32_
     if ((size_t)M * K * 2 > 0x7FFFFFFFu || (size_t)K / 8 * ((N + 15) / 16 * 16) * 4 > 0x7FFFFFFFu)
         return st::fail(ST_ERR_SHAPE, "st_gptq_i4_gemm: A or qweight above 2 GiB (M=%d K=%d N=%d); split M or N", M, K,
                         N);
-    const _Float16 *A = reinterpret_cast<const _Float16 *>(a);
-    if (perm) {
-        if (K > 32768) return st::fail(ST_ERR_SHAPE, "st_gptq_i4_gemm: act-order K=%d above 32768", K);
-        const size_t need = (size_t)M * K * sizeof(_Float16);
-        if (need > ctx->ws_bytes)
-            return st::fail(ST_ERR_WORKSPACE,
-                            "st_gptq_i4_gemm: act-order needs %zu B of workspace (st_context_reserve_workspace)", need);
-        _Float16 *Ap = reinterpret_cast<_Float16 *>(ctx->ws);
-        hipLaunchKernelGGL(permute_cols_kernel, dim3(M), dim3(256), (size_t)K * sizeof(_Float16), ctx->stream, A, perm, Ap,
-                           K);
-        if (int rc = st::launch_check("permute_cols_kernel")) return rc;
-        A = Ap;
-    }
+    if (K > 32768) return st::fail(ST_ERR_SHAPE, "st_gptq_i4_gemm: K=%d above 32768", K);
+    const size_t need = (size_t)M * K * sizeof(_Float16);
+    if (need > ctx->ws_bytes)
+        return st::fail(ST_ERR_WORKSPACE, "st_gptq_i4_gemm: needs %zu B of workspace for A (st_context_reserve_workspace)",
+                        need);
+    if (perm && !st::aligned16(perm)) return st::fail(ST_ERR_ALIGN, "st_gptq_i4_gemm: perm must be 16-byte aligned");
+    _Float16 *A = reinterpret_cast<_Float16 *>(ctx->ws);
+    hipLaunchKernelGGL(prep_a_kernel, dim3(M), dim3(256), (size_t)K * sizeof(_Float16), ctx->stream,
+                       reinterpret_cast<const _Float16 *>(a), perm, A, K);
+    if (int rc = st::launch_check("prep_a_kernel")) return rc;
     const int zoff = (flags & ST_FLAG_ZEROS_PLUS_ONE) ? 1 : 0;
     const bool f16out = c_dtype == ST_F16;
     if (flags & ST_FLAG_TILED) return launch_tiled<true>(ctx, A, qweight, scales, qzeros, zoff, c, f16out, M, K, N, group_size);

@@ -2,9 +2,11 @@
 a torch fp32 reference, through the C ABI.
 
 Bar: GEMM outputs within rel-L2 2e-3. The kernel
-keeps the dequant exact ((q - z) as f16 integers, the f16 scale applied to
-each group's f32 partial), so with f32 output it sits far below the bar;
-one-hot rows and integer-valued cases are checked bit for bit.
+forms (q - z) exactly and rounds (q - z) * s once to f16 per weight, then
+accumulates in f32 on MFMA; so it is checked three ways: against the f64
+oracle (bar 2e-3; typically ~2e-4), bit for bit on one-hot rows and integer
+cases (where it must equal the f16-rounded dequant), and against a torch fp32
+matmul over those f16-rounded weights (accumulation order only, ~1e-6).
 """
 import numpy as np
 import pytest
@@ -48,7 +50,7 @@ def test_gemm_matches_oracle(gpu, orc, tiled, Mr, K, N, gs, zeros, act):
     e = orc.rel_l2(y, ref)
     print(f"gemm M={Mr} K={K} N={N} gs={gs} zeros={zeros} act={act} tiled={tiled}: rel-L2 {e:.3e}")
     assert e < TOL
-    assert e < 1e-5  # exact dequant + f32 accumulation: far below the bar
+    assert e < 5e-4  # one f16 rounding per weight: ~2e-4
 
 
 @pytest.mark.parametrize("tiled", [True, False])
@@ -74,7 +76,8 @@ def test_gemm_one_hot_rows_are_dequant_rows(gpu, orc, tiled):
     for i, k in enumerate(ks):
         a[i, k] = 1.0
     y = run_gemm(gpu, w, a)
-    assert np.array_equal(y, W[ks]), "dequantized rows must be bit-exact"
+    W16 = W.astype(np.float16).astype(np.float32)  # (q - z) * s rounded once to f16
+    assert np.array_equal(y, W16[ks]), "one-hot rows must be the f16-rounded dequant, bit for bit"
 
 
 def test_gemm_integer_case_bit_equal(gpu, orc):
@@ -102,7 +105,7 @@ def test_gemm_agrees_with_decode_on_shared_rows(gpu, orc):
     sta.linear(gpu, x[:16].contiguous(), w, y_m)
     torch.cuda.synchronize()
     e = orc.rel_l2(y_g[:16].cpu().numpy(), y_m.cpu().numpy())
-    assert e < 1e-5
+    assert e < 1e-3  # matvec: exact dequant; GEMM: one f16 rounding per weight
 
 
 def test_gemm_full_config_vs_torch_fp32(gpu, orc):
@@ -122,9 +125,13 @@ def test_gemm_full_config_vs_torch_fp32(gpu, orc):
     ref = A[:, perm.long()].float() @ W
     torch.cuda.synchronize()
     e = (torch.linalg.vector_norm((C - ref).double()) / torch.linalg.vector_norm(ref.double())).item()
-    print(f"configs[3] gemm vs torch fp32: rel-L2 {e:.3e}")
+    ref16 = A[:, perm.long()].float() @ W.half().float()  # the kernel's f16-rounded weights
+    torch.cuda.synchronize()
+    e16 = (torch.linalg.vector_norm((C - ref16).double()) / torch.linalg.vector_norm(ref16.double())).item()
+    print(f"configs[3] gemm vs torch fp32: rel-L2 {e:.3e} (exact dequant), {e16:.3e} (f16-rounded dequant)")
     assert e < TOL
-    assert e < 1e-5
+    assert e < 5e-4
+    assert e16 < 1e-5
 
 
 def test_gemm_graph_replay_matches_eager(gpu, orc):
