@@ -5,7 +5,7 @@ include/shady_hip.h). This package is the host-side mirror of the
 reference's linear-layer interface (src/gpu.rs GpuContext, src/model.rs
 gptq_matvec / fused_silu_gptq_down, src/weights.rs QuantConfig).
 """
-from ._lib import ShadyHipError, header_symbols, lib  # noqa: F401
+from ._lib import ST_FLAG_TILED, ST_FLAG_ZEROS_PLUS_ONE, ShadyHipError, header_symbols, lib  # noqa: F401
 from .gpu import GpuContext  # noqa: F401
 from .model import (  # noqa: F401
     fused_gate_up_silu,
