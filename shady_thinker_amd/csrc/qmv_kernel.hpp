@@ -380,6 +380,7 @@ __global__ __launch_bounds__((64 * kMaxWavesFor<NSRC, COOP>)) void qmv_kernel(Pa
                 dst[0] = L2v;
                 dst[1] = L1v;
                 dst[2] = L0v;
+                dst[3] = u32x4{0, 0, 0, 0};  // row 4t+3 (see the zero fill below)
                 if (ii == 0) {
                     const int h = (sum + 32768) >> 16;
                     s_em[ui * M + m] = em;
@@ -390,8 +391,14 @@ __global__ __launch_bounds__((64 * kMaxWavesFor<NSRC, COOP>)) void qmv_kernel(Pa
         }
     };
 
-    // zero the A buffer once: rows 4t+3 and rows of absent tokens stay zero
-    for (int i = tt; i < afrags; i += span) abuf[i] = u32x4{0, 0, 0, 0};
+    // Rows of absent tokens must read as zero. COOP kernels (one token block)
+    // have none, and every other row is written by exactly one staging item
+    // (row 4t+3 included), so they need no fill: a fill by one wave would race
+    // with the staging writes of the others, there being no barrier between.
+    // The per-wave fallback zeroes its private region first (the same wave
+    // writes both, in order).
+    if constexpr (!COOP)
+        for (int i = tt; i < afrags; i += span) abuf[i] = u32x4{0, 0, 0, 0};
 
     // --------------------------------------------------------- main loop
     float tot[NSRC][MB];
