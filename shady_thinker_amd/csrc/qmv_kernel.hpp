@@ -175,6 +175,7 @@ template <int NSRC, bool COOP>
 constexpr int kMaxWavesFor = COOP ? (NSRC == 1 ? 16 : 8) : 4;
 
 constexpr int kCoopRounds = 2;  // x staging rounds per lane in COOP kernels (bounds M * K)
+constexpr int kScaleUnits = 8;  // groups per wave covered by the COOP scale block (one load per source)
 
 // Prefetch ring depth: the registers of weights in flight per lane, about 24
 // under a 128-VGPR budget (16-wave workgroups) and 40 for the dual kernel
@@ -182,6 +183,8 @@ constexpr int kCoopRounds = 2;  // x staging rounds per lane in COOP kernels (bo
 template <int FMT, int NSRC, int SPU, bool COOP>
 constexpr int ring_depth() {
     constexpr int WPU = (FMT == FMT_I8) ? 4 * SPU : 2 * SPU;
+    // (COOP keeps the depth it had with the scale in the ring: deeper rings
+    // measured slower, more registers and more loads queued at issue)
     constexpr int RPU = NSRC * (WPU + (FMT == FMT_I8 ? 0 : 1));
     constexpr int budget = (COOP && NSRC == 2) ? 40 : 24;
     return (budget / RPU) < 2 ? 2 : ((budget / RPU) > 6 ? 6 : (budget / RPU));
@@ -196,6 +199,7 @@ __global__ __launch_bounds__((64 * kMaxWavesFor<NSRC, COOP>)) void qmv_kernel(Pa
     // staging rounds per lane: per-wave chunk (fallback) or whole slice (COOP)
     constexpr int RMAX = COOP ? kCoopRounds : (4 * MB * IPU + 63) / 64;
 
+    constexpr bool SCB = COOP && FMT != FMT_I8;  // per-wave scale block (see below)
     const int tid = threadIdx.x;
     const int lane = tid & 63;
     const int wave = tid >> 6;
@@ -228,6 +232,8 @@ __global__ __launch_bounds__((64 * kMaxWavesFor<NSRC, COOP>)) void qmv_kernel(Pa
     int *s_nl = s_nh + CH * M;
     unsigned char *s_z = reinterpret_cast<unsigned char *>(s_nl + CH * M);
     const int zbase = COOP ? 0 : u0;  // unit index of s_z row 0
+    // COOP scale table: [wave][src][group - u0 (< kScaleUnits)][16 columns], after the reduction area
+    uint16_t *s_sc = reinterpret_cast<uint16_t *>(smem + (size_t)p.wave_lds + (size_t)NW * NSRC * MB * 64 * sizeof(float));
 
     // ------------------------------------------- zero points (before all loads)
     bool have_z[NSRC];
@@ -290,7 +296,7 @@ __global__ __launch_bounds__((64 * kMaxWavesFor<NSRC, COOP>)) void qmv_kernel(Pa
                     U.w[src][4 * st + 3] = t.w;
                 }
             }
-            if constexpr (FMT != FMT_I8) U.s[src] = p.sc[src][(size_t)u * N + ncol];
+            if constexpr (FMT != FMT_I8 && !COOP) U.s[src] = p.sc[src][(size_t)u * N + ncol];
         }
     };
 
@@ -451,7 +457,8 @@ __global__ __launch_bounds__((64 * kMaxWavesFor<NSRC, COOP>)) void qmv_kernel(Pa
                 if constexpr (FMT == FMT_I8) {
                     f = em;
                 } else {
-                    f = (float)__builtin_bit_cast(_Float16, U.s[src]) * em;
+                    const uint16_t sh = COOP ? s_sc[(wave * NSRC + src) * 128 + (u - u0) * 16 + c] : U.s[src];
+                    f = (float)__builtin_bit_cast(_Float16, sh) * em;
                     z = have_z[src] ? (int)s_z[((u - zbase) * NSRC + src) * 16 + c] : 8;
                 }
                 const int hi = S.x + __mul24(z, nh);
@@ -475,11 +482,29 @@ __global__ __launch_bounds__((64 * kMaxWavesFor<NSRC, COOP>)) void qmv_kernel(Pa
     // behind the weight ring), then the ring, all unconditionally.
     const int cs0 = COOP ? 0 : u0;
     if (COOP || u0 < u1) xload(cs0);
+    // COOP GPTQ: the scales of the wave's (at most kScaleUnits) groups for
+    // the tile's 16 columns in one 4-byte load per lane and source (lane l:
+    // group u0 + l / 8, columns 2 (l % 8) and +1), instead of one 2-byte
+    // load per group in the ring: half the ring's load instructions. Issued
+    // after x and before the ring, so waiting for them never waits for the
+    // ring; parked in LDS after the staging.
+    unsigned scw[NSRC];
+    if constexpr (SCB) {
+        const int ul = min(u0 + (lane >> 3), max(u1, 1) - 1);
+        const int cl = min(n0 + 2 * (lane & 7), N - 2);
+#pragma unroll
+        for (int src = 0; src < NSRC; ++src)
+            scw[src] = *reinterpret_cast<const unsigned *>(p.sc[src] + (size_t)ul * N + cl);
+    }
     if (u0 < u1) {
 #pragma unroll
         for (int d = 0; d < D; ++d) load_unit(ring[d], min(u0 + d, u1 - 1));
     }
     if (COOP || u0 < u1) stage(cs0);
+    if constexpr (SCB) {
+#pragma unroll
+        for (int src = 0; src < NSRC; ++src) reinterpret_cast<unsigned *>(s_sc)[(wave * NSRC + src) * 64 + lane] = scw[src];
+    }
     if constexpr (COOP) __syncthreads();
     if (u0 < u1) {
         int ui = COOP ? u0 : 0;  // A-buffer index of the current group
@@ -577,10 +602,16 @@ int launch_t(st_context *ctx, Params &p) {
         int nw = want >= 16 ? 16 : (want >= 8 ? 8 : 4);
         nw = std::max(4, std::min({nw, NWX, std::max(4, p.units)}));
         nw = std::max(4, std::min(NWX, env_int("ST_QMV_WAVES", nw)));
+        // GPTQ: at most kScaleUnits groups per wave (the scale block)
+        if (FMT != FMT_I8)
+            while ((p.units + nw - 1) / nw > kScaleUnits && nw < NWX) nw *= 2;
+        const bool scb_ok = FMT == FMT_I8 || (p.units + nw - 1) / nw <= kScaleUnits;
         const size_t ub = unit_bytes<FMT, NSRC, MB, SPU>(p);
-        const size_t lds = ((ub * p.units + 15) & ~size_t(15)) + (size_t)nw * NSRC * MB * 64 * sizeof(float);
+        const size_t lds = ((ub * p.units + 15) & ~size_t(15)) + (size_t)nw * NSRC * MB * 64 * sizeof(float) +
+                           (FMT != FMT_I8 ? (size_t)nw * NSRC * 64 * sizeof(unsigned) : 0);
         const long long items = (long long)p.M * p.units * IPU;
-        if (lds <= kCoopLdsBudget && items <= (long long)kCoopRounds * 64 * nw && !env_int("ST_QMV_NO_COOP", 0)) {
+        if (scb_ok && lds <= kCoopLdsBudget && items <= (long long)kCoopRounds * 64 * nw &&
+            !env_int("ST_QMV_NO_COOP", 0)) {
             p.nwaves = nw;
             p.wave_lds = (int)((ub * p.units + 15) & ~size_t(15));
             return launch_kernel<FMT, NSRC, XM, MB, SPU, PERM, true>(ctx, p, lds);
