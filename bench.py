@@ -178,7 +178,7 @@ def main():
     ap.add_argument("--no-gemm", action="store_true")
     ap.add_argument("--copy-calibrate", action="store_true",
                     help="profiling helper: 10 plain 64 MiB device copies (calibrates FETCH_SIZE / WRITE_SIZE)")
-    ap.add_argument("--only", default="", help="profiling helper: launch only this kernel, eagerly (q|gate_up|down)")
+    ap.add_argument("--only", default="", help="profiling helper: launch only this kernel, eagerly (q|gate_up|down|gemm|gemm512)")
     args = ap.parse_args()
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:
@@ -205,6 +205,18 @@ def main():
     gpu = sta.GpuContext(0)
     gen = torch.Generator(device=dev)
     gen.manual_seed(0)
+
+    if args.only in ("gemm", "gemm512"):  # eager GEMM loop for the profiler
+        K, N, Mr = 4096, 14336, (2048 if args.only == "gemm" else 512)
+        qw, sc = make_gptq(torch, dev, K, N, gen, gpu)
+        perm = torch.randperm(K, device=dev, generator=gen).to(torch.int32)
+        A = torch.randn(Mr, K, device=dev, generator=gen).half()
+        C = torch.empty(Mr, N, device=dev, dtype=torch.float16)
+        ms = time_loop(torch, lambda i: Mdl.gptq_gemm(gpu, A, qw, sc, C, K, N, GS, None, perm, sta.ST_FLAG_TILED),
+                       args.steps, args.warmup)
+        print(json.dumps({"only": args.only, "M": Mr, "steps": args.steps, "ms_eager": round(ms, 5),
+                          "TFLOP/s": round(2.0 * Mr * K * N / (ms * 1e-3) / 1e12, 1)}))
+        return
 
     H, I = 4096, 11008
     shapes = {"q": (H, H), "gate_up": (H, I), "down": (I, H)}
