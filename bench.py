@@ -314,6 +314,7 @@ def main():
 
     if not args.no_gemm:
         out["gemm"] = bench_gemm(torch, dev, gpu, Mdl, gen, args)
+    out["lm_head_bf16"] = bench_lm_head(torch, dev, gpu, Mdl, gen, args)
 
     if not args.no_cpu_baseline:
         out["cpu_baseline"] = cpu_baseline(args.cpu_seconds)
@@ -349,6 +350,21 @@ def bench_gemm(torch, dev, gpu, Mdl, gen, args):
         out[f"M{Mr}"] = {"ms": round(ms, 4), "TFLOP/s": round(tf, 1), "mfma_frac": round(tf / F16_MFMA_PEAK_TFLOPS, 4),
                          "torch_f16_gemm_TFLOP/s": round(2.0 * Mr * K * N / (ms_ref * 1e-3) / 1e12, 1)}
     return out
+
+
+def bench_lm_head(torch, dev, gpu, Mdl, gen, args):
+    """configs[4]'s lm_head: bf16 [151936, 2560] x f32 hidden, batch 1
+    (st_bf16_matvec; 778 MB, more than twice the MALL, so every call is cold)."""
+    K, N = 2560, 151936
+    w = (torch.randn(N, K, device=dev, generator=gen) * 0.02).to(torch.bfloat16).view(torch.int16)
+    x = torch.randn(1, K, device=dev, generator=gen)
+    y = torch.empty(1, N, device=dev)
+    iters = max(10, min(50, args.steps // 4))
+    ms = Replayer(torch, lambda i: Mdl.bf16_matvec(gpu, x, w, y, K, N), 1).run(iters, 3)
+    b = N * K * 2 + K * 4 + N * 4
+    del w
+    return {"N": N, "K": K, "ms": round(ms, 4), "bytes": b, "GB/s": round(b / (ms * 1e-3) / 1e9, 1),
+            "hbm_frac": round(b / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)}
 
 
 if __name__ == "__main__":

@@ -63,6 +63,8 @@ def lib():
             "orc_silu_gate_f64": (None, [_P, _P, _P, _I64]),
             "orc_int8_matvec_f64": (None, [_P, _P, _P, _I, _I, _I, _P]),
             "orc_gptq_matvec_4t_omp": (_I, [_P, _P, _P, _P, _I, _I, _I, _I]),
+            "orc_bf16_matvec_wgsl": (None, [_P, _P, _P, _I, _I, _I]),
+            "orc_bf16_matvec_f64": (None, [_P, _P, _I, _I, _I, _P]),
         }
         for name, (res, args) in sigs.items():
             fn = getattr(L, name)
@@ -231,6 +233,41 @@ def int8_matvec_f64(x, w, scale, K, N):
     y = np.empty((M, N), np.float64)
     lib().orc_int8_matvec_f64(_p(xd), _p(ww), _p(ss), M, K, N, _p(y))
     return y if xx.ndim > 1 else y[0]
+
+
+def bf16_matvec_wgsl(x, w, K, N, contract=1):
+    """bf16_matvec.wgsl order: x f32 [K], w bf16 bits uint16 [N, K] -> f32 [N]."""
+    xx = _c(x, np.float32)
+    ww = _c(w, np.uint16)
+    y = np.empty(N, np.float32)
+    lib().orc_bf16_matvec_wgsl(_p(xx), _p(ww), _p(y), K, N, contract)
+    return y
+
+
+def bf16_matvec_f64(x, w, K, N):
+    """x: [M, K] or [K] (any float dtype); w: bf16 bits uint16 [N, K]."""
+    xx = np.asarray(x)
+    M = 1 if xx.ndim == 1 else xx.shape[0]
+    xd = _c(xx.reshape(M, K), np.float64)
+    ww = _c(w, np.uint16)
+    y = np.empty((M, N), np.float64)
+    lib().orc_bf16_matvec_f64(_p(xd), _p(ww), M, K, N, _p(y))
+    return y if xx.ndim > 1 else y[0]
+
+
+def bf16_case(seed: int, K: int, N: int, M: int = 1, std=0.02):
+    """Seeded bf16 weight [N, K] ~N(0, std) (RNE to bf16) and f32 x ~N(0,1) [M, K]."""
+    base = seed * 16
+    wf = normal_f32(base + 1, N * K, 0.0, std)
+    w = np.array([f32_to_bf16(float(v)) for v in wf], np.uint16) if N * K <= 4096 else _bf16_bits(wf)
+    return {"K": K, "N": N, "w": w.reshape(N, K), "x": normal_f32(base + 5, M * K).reshape(M, K)}
+
+
+def _bf16_bits(f32: np.ndarray) -> np.ndarray:
+    """f32 -> bf16 bits, round to nearest even (finite inputs), vectorised."""
+    u = np.ascontiguousarray(f32, np.float32).view(np.uint32).astype(np.uint64)
+    r = (u + 0x7FFF + ((u >> 16) & 1)) >> 16
+    return r.astype(np.uint16)
 
 
 def gptq_matvec_4t_omp(x, qweight, scales, K, N, gs, threads=0):

@@ -423,6 +423,51 @@ ORC_API void orc_int8_matvec_f64(const double *x, const int8_t *w, const float *
     }
 }
 
+/* ----------------------------------------------------------- bf16 matvec */
+/* src/shaders/bf16_matvec.wgsl:15-18,21-72 (lm_head / tied embeddings):
+ * y[row] = sum_i bf16(W[row, i]) * x[i], W row-major [N, K] (two bf16 per u32,
+ * low half first), in the shader's order: packed words in blocks of four, then
+ * the remainder, one f32 multiply-add per element (contract = 1: fused, as a
+ * driver contracting `sum += a * b`; 0: separate multiply and add). */
+static inline float orc_bf16_to_f32(uint16_t b) {
+    uint32_t u = (uint32_t)b << 16;
+    float f;
+    memcpy(&f, &u, 4);
+    return f;
+}
+
+ORC_API void orc_bf16_matvec_wgsl(const float *x, const uint16_t *w, float *y, int K, int N, int contract) {
+#pragma omp parallel for schedule(static)
+    for (int row = 0; row < N; row++) {
+        const uint16_t *wr = w + (int64_t)row * K;
+        float sum = 0.0f;
+        for (int i = 0; i < K; i++) {
+            const float a = orc_bf16_to_f32(wr[i]);
+            if (contract)
+                sum = fmaf(a, x[i], sum);
+            else {
+                const volatile float prod = a * x[i];
+                sum = sum + prod;
+            }
+        }
+        y[row] = sum;
+    }
+}
+
+/* f64 truth for the bf16 matvec, M rows of x ([M, K]) -> y [M, N]. */
+ORC_API void orc_bf16_matvec_f64(const double *x, const uint16_t *w, int M, int K, int N, double *y) {
+#pragma omp parallel for schedule(static)
+    for (int n = 0; n < N; n++) {
+        const uint16_t *wr = w + (int64_t)n * K;
+        for (int m = 0; m < M; m++) {
+            const double *xr = x + (int64_t)m * K;
+            double acc = 0.0;
+            for (int k = 0; k < K; k++) acc += (double)orc_bf16_to_f32(wr[k]) * xr[k];
+            y[(int64_t)m * N + n] = acc;
+        }
+    }
+}
+
 /* -------------------------------------------------------- CPU baseline */
 /* gptq_matvec_4t restated (src/shaders/gptq_matvec_4t.wgsl:37-85), OpenMP
  * over columns on `threads` host threads; the timed CPU baseline when the

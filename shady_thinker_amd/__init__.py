@@ -8,6 +8,7 @@ gptq_matvec / fused_silu_gptq_down, src/weights.rs QuantConfig).
 from ._lib import ST_FLAG_TILED, ST_FLAG_ZEROS_PLUS_ONE, ShadyHipError, header_symbols, lib  # noqa: F401
 from .gpu import GpuContext  # noqa: F401
 from .model import (  # noqa: F401
+    bf16_matvec,
     fused_gate_up_silu,
     fused_silu_gptq_down,
     gptq_dequant,

@@ -97,6 +97,18 @@ def gptq_gemm(gpu, a, qweight, scales, c, k: int, n: int, group_size: int = 128,
          k, n, group_size, flags)
 
 
+def bf16_matvec(gpu, x, w, y, k: int, n: int) -> None:
+    """y[M, n] = x[M, k] . w^T, w bf16 [n, k] (Model::bf16_lm_head,
+    src/model.rs:455-468 / bf16_matvec.wgsl). x f32 or f16, y f32, M <= 4."""
+    import torch
+
+    m = _rows(x, k)
+    if w.dtype not in (torch.bfloat16, torch.int16, torch.uint16):
+        raise TypeError(f"bf16 weight dtype {w.dtype}")
+    gpu.sync_stream()
+    call("st_bf16_matvec", gpu.handle, ptr(x), _xdtype(x), ptr(w), ptr(y), m, k, n)
+
+
 # ---------------------------------------------------------- weight objects
 def linear(gpu, x, w, y) -> None:
     """Dispatch on the weight type: GptqWeight -> st_gptq_i4_matvec (M <= 32)

@@ -265,3 +265,28 @@ def test_golden_fixtures_reproduce(orc):
                                     qzeros=d["qzeros"] if d["qzeros"].size else None,
                                     g_idx=d["g_idx"] if d["g_idx"].size else None)
         assert np.array_equal(y, d["y"]), f
+
+
+def test_bf16_matvec_oracle_pins(orc):
+    """bf16 matvec oracle: f64 truth equals numpy float64 on the exact f32
+    values of the bf16 bits; the WGSL-order f32 path equals it bit for bit on
+    an integer-exact case (small integer weights and x) and stays within
+    1e-6 rel-L2 on random data; bf16 generation is RNE (matches torch)."""
+    import torch
+
+    K, N = 136, 40
+    c = orc.bf16_case(5, K, N, 2)
+    Wf = (c["w"].astype(np.uint32) << 16).view(np.float32).astype(np.float64)
+    ref = c["x"].astype(np.float64) @ Wf.T
+    assert np.allclose(orc.bf16_matvec_f64(c["x"], c["w"], K, N), ref, rtol=1e-12, atol=1e-12)
+    for contract in (0, 1):
+        wg = orc.bf16_matvec_wgsl(c["x"][0], c["w"], K, N, contract)
+        assert orc.rel_l2(wg, ref[0]) < 1e-6
+    rng = np.random.default_rng(1)
+    wi = rng.integers(-8, 9, size=(N, K)).astype(np.float32)
+    xi = rng.integers(-4, 5, size=K).astype(np.float32)
+    wbits = orc._bf16_bits(wi)
+    exact = orc.bf16_matvec_f64(xi, wbits, K, N)
+    assert np.array_equal(orc.bf16_matvec_wgsl(xi, wbits, K, N).astype(np.float64), exact)
+    v = rng.standard_normal(4096).astype(np.float32)
+    assert np.array_equal(orc._bf16_bits(v), torch.from_numpy(v).to(torch.bfloat16).view(torch.int16).numpy().view(np.uint16))
