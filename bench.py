@@ -176,6 +176,7 @@ def main():
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-gemm", action="store_true")
+    ap.add_argument("--no-stack", action="store_true", help="skip the configs[4] 36-layer linear stack")
     ap.add_argument("--copy-calibrate", action="store_true",
                     help="profiling helper: 10 plain 64 MiB device copies (calibrates FETCH_SIZE / WRITE_SIZE)")
     ap.add_argument("--only", default="", help="profiling helper: launch only this kernel, eagerly (q|gate_up|down|gemm|gemm512)")
@@ -315,6 +316,8 @@ def main():
     if not args.no_gemm:
         out["gemm"] = bench_gemm(torch, dev, gpu, Mdl, gen, args)
     out["lm_head_bf16"] = bench_lm_head(torch, dev, gpu, Mdl, gen, args)
+    if not args.no_stack:
+        out["stack_cfg4"] = bench_stack(torch, dev, gpu, Mdl, gen, args)
 
     if not args.no_cpu_baseline:
         out["cpu_baseline"] = cpu_baseline(args.cpu_seconds)
@@ -350,6 +353,70 @@ def bench_gemm(torch, dev, gpu, Mdl, gen, args):
         out[f"M{Mr}"] = {"ms": round(ms, 4), "TFLOP/s": round(tf, 1), "mfma_frac": round(tf / F16_MFMA_PEAK_TFLOPS, 4),
                          "torch_f16_gemm_TFLOP/s": round(2.0 * Mr * K * N / (ms_ref * 1e-3) / 1e12, 1)}
     return out
+
+
+def bench_stack(torch, dev, gpu, Mdl, gen, args):
+    """the quantized linear stack of a 36-layer decoder
+    (hidden 2560, 32 q / 8 kv heads of 128, intermediate 9728, vocab 151936),
+    every linear GPTQ int4 g128 (lm_head included), random-init packed
+    weights (2.07 GB: each token streams them from HBM). A token = per layer
+    q, k, v, o, fused gate/up (silu(g)*u) and down on it, then the lm_head;
+    captured as one HIP graph and replayed; batch 1 and 16. Attention and
+    norms are outside the path, so activations are synthetic and fixed."""
+    H, Q, KV, I, V, L = 2560, 4096, 1024, 9728, 151936, 36
+    TF = sta_flags_tiled()
+    layers = []
+    for _ in range(L):
+        layers.append({"q": make_gptq(torch, dev, H, Q, gen, gpu), "k": make_gptq(torch, dev, H, KV, gen, gpu),
+                       "v": make_gptq(torch, dev, H, KV, gen, gpu), "o": make_gptq(torch, dev, Q, H, gen, gpu),
+                       "g": make_gptq(torch, dev, H, I, gen, gpu), "u": make_gptq(torch, dev, H, I, gen, gpu),
+                       "d": make_gptq(torch, dev, I, H, gen, gpu)})
+    lm = make_gptq(torch, dev, H, V, gen, gpu)
+    per_layer = (decode_bytes(H, Q, 4, Q) + 2 * decode_bytes(H, KV, 4, KV) + decode_bytes(Q, H, 4, H) +
+                 decode_bytes(H, 2 * I, 4, I) + decode_bytes(I, H, 4, H))
+    out = {"layers": L, "weights_GB": None}
+    wbytes = 0
+    for Mb in (1, 16):
+        x = torch.randn(Mb, H, device=dev, generator=gen)
+        attn = torch.randn(Mb, Q, device=dev, generator=gen)
+        yq = torch.empty(Mb, Q, device=dev)
+        yk = torch.empty(Mb, KV, device=dev)
+        yv = torch.empty(Mb, KV, device=dev)
+        yo = torch.empty(Mb, H, device=dev)
+        h = torch.empty(Mb, I, device=dev)
+        yd = torch.empty(Mb, H, device=dev)
+        logits = torch.empty(Mb, V, device=dev)
+
+        def token(i):
+            for w in layers:
+                Mdl.gptq_matvec(gpu, "q_proj", x, w["q"][0], w["q"][1], yq, H, Q, GS, flags=TF)
+                Mdl.gptq_matvec(gpu, "k_proj", x, w["k"][0], w["k"][1], yk, H, KV, GS, flags=TF)
+                Mdl.gptq_matvec(gpu, "v_proj", x, w["v"][0], w["v"][1], yv, H, KV, GS, flags=TF)
+                Mdl.gptq_matvec(gpu, "o_proj", attn, w["o"][0], w["o"][1], yo, Q, H, GS, flags=TF)
+                Mdl.fused_gate_up_silu(gpu, x, w["g"][0], w["g"][1], w["u"][0], w["u"][1], h, H, I, GS, flags=TF)
+                Mdl.gptq_matvec(gpu, "down_proj", h, w["d"][0], w["d"][1], yd, I, H, GS, flags=TF)
+            Mdl.gptq_matvec(gpu, "lm_head", x, lm[0], lm[1], logits, H, V, GS, flags=TF)
+
+        iters = max(10, min(50, args.steps // 4))
+        ms = Replayer(torch, token, 1).run(iters, 3)
+        # algorithmic bytes of one step: the weights (read once for all Mb
+        # tokens) plus batch-1 activation terms (Mb - 1 more rows are < 0.1%)
+        tok_bytes = L * per_layer + decode_bytes(H, V, 4, V)
+        wbytes = tok_bytes
+        out[f"batch{Mb}"] = {"ms_per_token_step": round(ms, 4), "tokens_per_s": round(Mb / (ms * 1e-3), 1),
+                             "GB/s": round(tok_bytes / (ms * 1e-3) / 1e9, 1),
+                             "hbm_frac": round(tok_bytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+                             "kernels_per_step": 6 * L + 1}
+    out["weights_GB"] = round(wbytes / 1e9, 3)
+    del layers, lm
+    torch.cuda.empty_cache()
+    return out
+
+
+def sta_flags_tiled():
+    from shady_thinker_amd._lib import ST_FLAG_TILED
+
+    return ST_FLAG_TILED
 
 
 def bench_lm_head(torch, dev, gpu, Mdl, gen, args):

@@ -176,8 +176,8 @@ int st_gptq_i4_act_order(st_context *ctx, const uint32_t *qweight, const int32_t
                          int group_size);
 
 /* bf16 matvec: y[M, N] = x[M, K] . W^T, W bf16 row-major [N, K] (two bf16 per
- * u32, low half first), x f32 or f16 (x_dtype), y f32, 1 <= M <= 4,
- * K % 8 == 0, K <= 10240. Replaces src/shaders/bf16_matvec.wgsl:21-72 (the
+ * u32, low half first), x f32 or f16 (x_dtype), y f32, 1 <= M <= 8,
+ * K % 8 == 0, K <= 10240 (M <= 4) or 5120 (M <= 8). Replaces src/shaders/bf16_matvec.wgsl:21-72 (the
  * lm_head / tied-embedding projection, dispatched at src/model.rs:455-468
  * and :824-831); f32 accumulation, results within 1e-4 rel-L2 of f64. */
 int st_bf16_matvec(st_context *ctx, const void *x, int x_dtype, const uint16_t *w, float *y, int M, int K,

@@ -1,6 +1,6 @@
 // bf16 matvec for the lm_head / tied embeddings: y[m, n] = sum_k bf16(W[n, k])
 // * x[m, k], W row-major [N, K] (two bf16 per u32, low half first), x f32 or
-// f16 [M, K], y f32 [M, N], M <= 4. Replaces src/shaders/bf16_matvec.wgsl:21-72
+// f16 [M, K], y f32 [M, N], M <= 8. Replaces src/shaders/bf16_matvec.wgsl:21-72
 // (dispatched at src/model.rs:455-468, 824-831).
 //
 // A pure HBM stream (151936 x 2560 bf16 = 778 MB for one token of configs[4]);
@@ -145,7 +145,8 @@ int launch(st_context *ctx, const void *x, const uint16_t *w, float *y, int M, i
 template <bool F16X>
 int by_m(st_context *ctx, const void *x, const uint16_t *w, float *y, int M, int K, int N) {
     if (M == 1) return launch<1, F16X>(ctx, x, w, y, M, K, N);
-    return launch<4, F16X>(ctx, x, w, y, M, K, N);
+    if (M <= 4) return launch<4, F16X>(ctx, x, w, y, M, K, N);
+    return launch<8, F16X>(ctx, x, w, y, M, K, N);
 }
 
 }  // namespace
@@ -153,10 +154,11 @@ int by_m(st_context *ctx, const void *x, const uint16_t *w, float *y, int M, int
 extern "C" int st_bf16_matvec(st_context *ctx, const void *x, int x_dtype, const uint16_t *w, float *y, int M, int K,
                               int N) {
     if (!ctx || !x || !w || !y) return st::fail(ST_ERR_INVALID, "st_bf16_matvec: NULL argument");
-    if (M < 1 || M > 4) return st::fail(ST_ERR_SHAPE, "st_bf16_matvec: M=%d not in [1,4]", M);
+    if (M < 1 || M > 8) return st::fail(ST_ERR_SHAPE, "st_bf16_matvec: M=%d not in [1,8]", M);
     if (K <= 0 || K % 8 || N <= 0) return st::fail(ST_ERR_SHAPE, "st_bf16_matvec: K=%d (multiple of 8), N=%d", K, N);
-    if ((size_t)4 * K * sizeof(float) > 160 * 1024)
-        return st::fail(ST_ERR_SHAPE, "st_bf16_matvec: K=%d too large for the LDS x copy", K);
+    const int mt = M == 1 ? 1 : (M <= 4 ? 4 : 8);  // token rows of the LDS x copy
+    if ((size_t)mt * K * sizeof(float) > 160 * 1024)
+        return st::fail(ST_ERR_SHAPE, "st_bf16_matvec: M=%d K=%d too large for the LDS x copy", M, K);
     if (x_dtype != ST_F32 && x_dtype != ST_F16) return st::fail(ST_ERR_INVALID, "st_bf16_matvec: x_dtype %d", x_dtype);
     if (!st::aligned16(w) || !st::aligned16(x))
         return st::fail(ST_ERR_ALIGN, "st_bf16_matvec: x and w must be 16-byte aligned");

@@ -99,7 +99,7 @@ def gptq_gemm(gpu, a, qweight, scales, c, k: int, n: int, group_size: int = 128,
 
 def bf16_matvec(gpu, x, w, y, k: int, n: int) -> None:
     """y[M, n] = x[M, k] . w^T, w bf16 [n, k] (Model::bf16_lm_head,
-    src/model.rs:455-468 / bf16_matvec.wgsl). x f32 or f16, y f32, M <= 4."""
+    src/model.rs:455-468 / bf16_matvec.wgsl). x f32 or f16, y f32, M <= 8."""
     import torch
 
     m = _rows(x, k)

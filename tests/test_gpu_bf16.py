@@ -27,7 +27,7 @@ def run(gpu, w_bits, x, xdtype=torch.float32):
 
 
 @pytest.mark.parametrize("K,N,Mr", [(64, 8, 1), (72, 13, 1), (2560, 1000, 1), (2560, 1000, 2), (1032, 777, 4),
-                                    (4096, 4099, 3)])
+                                    (4096, 4099, 3), (2560, 600, 8), (520, 33, 5)])
 def test_bf16_matvec_matches_oracle(gpu, orc, K, N, Mr):
     c = orc.bf16_case(20 + K + Mr, K, N, Mr)
     y = run(gpu, c["w"], c["x"])
@@ -84,10 +84,10 @@ def test_bf16_lm_head_full_size_vs_torch(gpu):
 
 def test_bf16_errors(gpu):
     w = torch.zeros(8, 64, dtype=torch.int16, device=gpu.device)
-    x = torch.zeros(5, 64, device=gpu.device)
-    y = torch.empty(5, 8, device=gpu.device)
+    x = torch.zeros(9, 64, device=gpu.device)
+    y = torch.empty(9, 8, device=gpu.device)
     with pytest.raises(sta.ShadyHipError):
-        M.bf16_matvec(gpu, x, w, y, 64, 8)  # M = 5
+        M.bf16_matvec(gpu, x, w, y, 64, 8)  # M = 9
     w2 = torch.zeros(8, 60, dtype=torch.int16, device=gpu.device)
     with pytest.raises(sta.ShadyHipError):
         M.bf16_matvec(gpu, x[:1, :60].contiguous(), w2, y[:1], 60, 8)  # K % 8
