@@ -17,4 +17,5 @@ from .model import (  # noqa: F401
     int8_matvec,
     linear,
 )
+from .loader import load_gptq_checkpoint, read_gptq_checkpoint  # noqa: F401
 from .weights import GptqWeight, Int8Weight, QuantConfig  # noqa: F401
