@@ -316,6 +316,7 @@ def main():
     if not args.no_gemm:
         out["gemm"] = bench_gemm(torch, dev, gpu, Mdl, gen, args)
     out["lm_head_bf16"] = bench_lm_head(torch, dev, gpu, Mdl, gen, args)
+    out["int8_cfg2"] = bench_int8(torch, dev, gpu, Mdl, gen, args)
     if not args.no_stack:
         out["stack_cfg4"] = bench_stack(torch, dev, gpu, Mdl, gen, args)
 
@@ -407,6 +408,35 @@ def bench_stack(torch, dev, gpu, Mdl, gen, args):
                              "GB/s": round(tok_bytes / (ms * 1e-3) / 1e9, 1),
                              "hbm_frac": round(tok_bytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
                              "kernels_per_step": 6 * L + 1}
+    # Prefill of a 512-token prompt through the same weights with the GEMM
+    # (f16 activations and outputs; q, k, v, o, gate, up, down per layer),
+    # then the lm_head for the last token only, as a prefill does.
+    P = 512
+    xa = torch.randn(P, H, device=dev, generator=gen).half()
+    aa = torch.randn(P, Q, device=dev, generator=gen).half()
+    ha = torch.randn(P, I, device=dev, generator=gen).half()
+    cq = torch.empty(P, Q, device=dev, dtype=torch.float16)
+    ckv = torch.empty(P, KV, device=dev, dtype=torch.float16)
+    ch = torch.empty(P, H, device=dev, dtype=torch.float16)
+    ci = torch.empty(P, I, device=dev, dtype=torch.float16)
+    xl = torch.randn(1, H, device=dev, generator=gen)
+    logits1 = torch.empty(1, V, device=dev)
+
+    def prefill(i):
+        for w in layers:
+            Mdl.gptq_gemm(gpu, xa, w["q"][0], w["q"][1], cq, H, Q, GS, None, None, TF)
+            Mdl.gptq_gemm(gpu, xa, w["k"][0], w["k"][1], ckv, H, KV, GS, None, None, TF)
+            Mdl.gptq_gemm(gpu, xa, w["v"][0], w["v"][1], ckv, H, KV, GS, None, None, TF)
+            Mdl.gptq_gemm(gpu, aa, w["o"][0], w["o"][1], ch, Q, H, GS, None, None, TF)
+            Mdl.gptq_gemm(gpu, xa, w["g"][0], w["g"][1], ci, H, I, GS, None, None, TF)
+            Mdl.gptq_gemm(gpu, xa, w["u"][0], w["u"][1], ci, H, I, GS, None, None, TF)
+            Mdl.gptq_gemm(gpu, ha, w["d"][0], w["d"][1], ch, I, H, GS, None, None, TF)
+        Mdl.gptq_matvec(gpu, "lm_head", xl, lm[0], lm[1], logits1, H, V, GS, flags=TF)
+
+    ms = Replayer(torch, prefill, 1).run(max(3, min(10, args.steps // 20)), 1)
+    flops = 2.0 * P * L * (H * Q + 2 * H * KV + Q * H + 2 * H * I + I * H)
+    out[f"prefill{P}"] = {"ms": round(ms, 3), "tokens_per_s": round(P / (ms * 1e-3), 1),
+                          "TFLOP/s": round(flops / (ms * 1e-3) / 1e12, 1), "gemm_calls": 7 * L}
     out["weights_GB"] = round(wbytes / 1e9, 3)
     del layers, lm
     torch.cuda.empty_cache()
@@ -417,6 +447,26 @@ def sta_flags_tiled():
     from shady_thinker_amd._lib import ST_FLAG_TILED
 
     return ST_FLAG_TILED
+
+
+def bench_int8(torch, dev, gpu, Mdl, gen, args):
+    """INT8 per-channel weights [13824, 5120] (70.8 MB), f16
+    activations, M = 1 / 8 / 32 (matvec to skinny GEMM), 4 cold copies."""
+    K, N, copies = 5120, 13824, 4
+    ws = [torch.randint(-127, 128, (N, K), device=dev, dtype=torch.int8, generator=gen) for _ in range(copies)]
+    sc = (torch.randn(N, device=dev, generator=gen) * 0.01).abs()
+    out = {"K": K, "N": N}
+    for Mr in (1, 8, 32):
+        x = torch.randn(Mr, K, device=dev, generator=gen).half()
+        y = torch.empty(Mr, N, device=dev)
+        iters = max(20, min(100, args.steps // 2))
+        ms = Replayer(torch, lambda i: Mdl.int8_matvec(gpu, x, ws[i % copies], sc, y, K, N), copies).run(iters, 4)
+        b = K * N + 4 * N + 2 * Mr * K + 4 * Mr * N
+        out[f"M{Mr}"] = {"ms": round(ms, 5), "GB/s": round(b / (ms * 1e-3) / 1e9, 1),
+                         "hbm_frac": round(b / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+                         "TOPS": round(2.0 * Mr * K * N / (ms * 1e-3) / 1e12, 2)}
+    del ws
+    return out
 
 
 def bench_lm_head(torch, dev, gpu, Mdl, gen, args):

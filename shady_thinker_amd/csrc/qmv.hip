@@ -52,6 +52,30 @@ int launch_i4(st_context *ctx, QmvParams &p, bool tiled, int nsrc, int xm) {
     return p.perm ? dispatch<FMT_I4, true>(ctx, p, nsrc, xm) : dispatch<FMT_I4, false>(ctx, p, nsrc, xm);
 }
 
+// Calls with more than kTokenBlock tokens run as blocks of kTokenBlock: the
+// per-wave staging of the multi-token kernels grows with M * K per wave, and
+// at 32 tokens two blocks of 16 (or eight of 4) measured several times
+// faster than one launch, even though every block streams the weights again.
+// (A skinny-GEMM kernel that reuses the weights across blocks is the better
+// design for M > 4.)
+constexpr int kTokenBlock = 16;
+
+template <typename F>
+int by_token_blocks(QmvParams &p, int xm, F &&launch) {
+    const int blk = std::max(1, st::qmv::env_int("ST_QMV_BLOCK", kTokenBlock));
+    if (p.M <= blk) return launch(p);
+    const size_t xe = xm == XM_F16 ? 2 : 4;
+    for (int m0 = 0; m0 < p.M; m0 += blk) {
+        QmvParams q = p;
+        q.M = std::min(blk, p.M - m0);
+        q.x = static_cast<const char *>(p.x) + (size_t)m0 * p.K * xe;
+        if (p.xb) q.xb = p.xb + (size_t)m0 * p.K;
+        q.y = p.y + (size_t)m0 * p.N;
+        if (int rc = launch(q)) return rc;
+    }
+    return ST_OK;
+}
+
 int check_i4(const char *fn, int M, int K, int N, int gs, int mmax) {
     if (gs != 64 && gs != 128 && gs != 256)
         return st::fail(ST_ERR_SHAPE, "%s: group_size %d not in {64,128,256}", fn, gs);
@@ -88,7 +112,8 @@ int st_gptq_i4_matvec(st_context *ctx, const void *x, int x_dtype, const uint32_
     p.gs = group_size;
     p.zoff = (flags & ST_FLAG_ZEROS_PLUS_ONE) ? 1 : 0;
     const bool tiled = flags & ST_FLAG_TILED;
-    return launch_i4(ctx, p, tiled, 1, x_dtype == ST_F32 ? XM_F32 : XM_F16);
+    const int xm = x_dtype == ST_F32 ? XM_F32 : XM_F16;
+    return by_token_blocks(p, xm, [&](QmvParams &q) { return launch_i4(ctx, q, tiled, 1, xm); });
 }
 
 int st_gptq_i4_silu_matvec(st_context *ctx, const float *a, const float *b, const uint32_t *qweight,
@@ -112,7 +137,8 @@ int st_gptq_i4_silu_matvec(st_context *ctx, const float *a, const float *b, cons
     p.N = N;
     p.gs = group_size;
     p.zoff = (flags & ST_FLAG_ZEROS_PLUS_ONE) ? 1 : 0;
-    return launch_i4(ctx, p, flags & ST_FLAG_TILED, 1, XM_SILU);
+    const bool tiled = flags & ST_FLAG_TILED;
+    return by_token_blocks(p, XM_SILU, [&](QmvParams &q) { return launch_i4(ctx, q, tiled, 1, XM_SILU); });
 }
 
 int st_gptq_i4_gate_up_silu(st_context *ctx, const void *x, int x_dtype, const uint32_t *qweight_gate,
@@ -145,7 +171,8 @@ int st_gptq_i4_gate_up_silu(st_context *ctx, const void *x, int x_dtype, const u
     p.gs = group_size;
     p.zoff = (flags & ST_FLAG_ZEROS_PLUS_ONE) ? 1 : 0;
     const bool tiled = flags & ST_FLAG_TILED;
-    return launch_i4(ctx, p, tiled, 2, x_dtype == ST_F32 ? XM_F32 : XM_F16);
+    const int xm = x_dtype == ST_F32 ? XM_F32 : XM_F16;
+    return by_token_blocks(p, xm, [&](QmvParams &q) { return launch_i4(ctx, q, tiled, 2, xm); });
 }
 
 size_t st_gptq_i4_tiled_words(int K, int N, int group_size) {
@@ -186,7 +213,8 @@ int st_int8_matvec(st_context *ctx, const void *x, int x_dtype, const int8_t *w,
     p.gs = 128;
     p.units = K / 128;
     p.ntiles = (N + kTileN - 1) / kTileN;
-    return dispatch<FMT_I8, false>(ctx, p, 1, x_dtype == ST_F32 ? XM_F32 : XM_F16);
+    const int xm = x_dtype == ST_F32 ? XM_F32 : XM_F16;
+    return by_token_blocks(p, xm, [&](QmvParams &q) { return dispatch<FMT_I8, false>(ctx, q, 1, xm); });
 }
 
 }  // extern "C"
