@@ -36,6 +36,7 @@
 #include "common.hpp"
 
 #include <algorithm>
+#include <cstdlib>
 #include <type_traits>
 
 namespace {
@@ -96,7 +97,8 @@ __device__ __forceinline__ half8 word_to_b(unsigned w, const BConv &c) {
 template <int GS, bool TILED, bool F16OUT>
 __global__ __launch_bounds__(kThreads, kWavesPerSimd) void gemm_kernel(const _Float16 *__restrict__ A, const uint32_t *__restrict__ qw,
                                                            const uint16_t *__restrict__ sc, const uint32_t *__restrict__ qz,
-                                                           int zoff, void *__restrict__ C, int M, int K, int N) {
+                                                           int zoff, void *__restrict__ C, int M, int K, int N,
+                                                           int kps, float *__restrict__ part) {
     // Two separate arrays (not one [2][...]) so that alias analysis can tell
     // the stage being read from the stage the DMA is filling; otherwise every
     // LDS read waits for the in-flight DMA.
@@ -112,7 +114,10 @@ __global__ __launch_bounds__(kThreads, kWavesPerSimd) void gemm_kernel(const _Fl
     // XCD-major tile order: consecutive ids run on the same XCD.
     const int MT = (M + BM - 1) / BM, NT = (N + BN - 1) / BN;
     const int T = MT * NT;
-    const int b = blockIdx.x;
+    // split-K: workgroup b takes K tiles [kt0, kt1) of tile b % T (kps is
+    // even whenever it is not all of K, so a split starts on a group of 256)
+    const int split = blockIdx.x / T;
+    const int b = blockIdx.x % T;
     const int id = (T % 8 == 0) ? (b % 8) * (T / 8) + b / 8 : b;
     const int mt = id / NT, nt = id % NT;
     const int m0 = mt * BM, n0 = nt * BN;
@@ -124,6 +129,7 @@ __global__ __launch_bounds__(kThreads, kWavesPerSimd) void gemm_kernel(const _Fl
     for (int cb = 0; cb < CB; ++cb) col[cb] = min(nw + 32 * cb + l32, N - 1);
 
     const int ntiles = K / KT;
+    const int kt0 = split * kps, kt1 = min(kt0 + kps, ntiles);
 
     // ---------------------------------------------------------------- loads
     // Buffer loads: one scalar resource per operand, a 32-bit per-lane
@@ -249,15 +255,16 @@ __global__ __launch_bounds__(kThreads, kWavesPerSimd) void gemm_kernel(const _Fl
         }
     };
 
-    load_groups(0, 0);
-    a_dma(std::integral_constant<int, 0>{}, 0);
-    load_b(bw[0], 0);
+    load_groups(0, kt0);
+    a_dma(std::integral_constant<int, 0>{}, kt0);
+    load_b(bw[0], kt0);
     __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): this wave's DMAs are in LDS
     __syncthreads();
 
-    // One K tile from LDS buffer BUF = kt & 1. The tile loop is unrolled by
-    // two so that the register buffer index and the group boundaries are
-    // compile-time (kt * KT mod GS depends only on BUF for GS <= 2 KT).
+    // One K tile from LDS buffer BUF = (kt - kt0) & 1. The tile loop is
+    // unrolled by two so that the register buffer index and the group
+    // boundaries are compile-time (kt * KT mod GS depends only on BUF for
+    // GS <= 2 KT, kt0 being even).
     // Software pipeline over the 8 k-steps: the A fragments (LDS) and the
     // converted B of step t + 1 are produced while step t's MFMAs run.
     auto tile = [&](auto BUFC, int kt) {
@@ -266,7 +273,7 @@ __global__ __launch_bounds__(kThreads, kWavesPerSimd) void gemm_kernel(const _Fl
         // tile reloads itself into the idle stage): with no branch around
         // them, the compiler's wait counting never sees a path on which a
         // previous tile's loads are still in flight.
-        const int kn = min(kt + 1, ntiles - 1);
+        const int kn = min(kt + 1, kt1 - 1);
         load_groups(BUF ^ 1, kn);
         a_dma(std::integral_constant<int, BUF ^ 1>{}, kn);  // stage BUF ^ 1 was last read before the previous barrier
         load_b(bw[BUF ^ 1], kn);
@@ -298,10 +305,11 @@ __global__ __launch_bounds__(kThreads, kWavesPerSimd) void gemm_kernel(const _Fl
         __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): next tile's A DMAs (and B words) landed
         __syncthreads();
     };
-    // K % 256 == 0 when GS == 256, so a group never ends on an odd last tile.
-    for (int kt = 0; kt < ntiles; kt += 2) {
+    // K % 256 == 0 when GS == 256 and kps is even, so a group never ends on
+    // an odd last tile.
+    for (int kt = kt0; kt < kt1; kt += 2) {
         tile(std::integral_constant<int, 0>{}, kt);
-        if (kt + 1 < ntiles) tile(std::integral_constant<int, 1>{}, kt + 1);
+        if (kt + 1 < kt1) tile(std::integral_constant<int, 1>{}, kt + 1);
     }
 
     // ------------------------------------------------------------ output
@@ -316,7 +324,9 @@ __global__ __launch_bounds__(kThreads, kWavesPerSimd) void gemm_kernel(const _Fl
             for (int i = 0; i < 16; ++i) {
                 const int m = m0 + mw + rb * 32 + 8 * (i >> 2) + 4 * hi + (i & 3);
                 if (m >= M) continue;
-                if constexpr (F16OUT)
+                if (part)  // split-K: this split's f32 partial
+                    part[((size_t)split * M + m) * N + n] = acc[rb][cb][i];
+                else if constexpr (F16OUT)
                     static_cast<_Float16 *>(C)[(size_t)m * N + n] = (_Float16)acc[rb][cb][i];
                 else
                     static_cast<float *>(C)[(size_t)m * N + n] = acc[rb][cb][i];
@@ -363,27 +373,93 @@ __global__ __launch_bounds__(256) void prep_a_kernel(const _Float16 *__restrict_
     }
 }
 
+// C[m, n] = sum over s < S of part[s, m, n] (fixed order: deterministic).
+template <bool F16OUT>
+__global__ __launch_bounds__(256) void splitk_reduce_kernel(const float *__restrict__ part, void *__restrict__ C,
+                                                            size_t MN, int S) {
+    const size_t i = ((size_t)blockIdx.x * 256 + threadIdx.x) * 4;
+    if (i >= MN) return;  // MN % 4 == 0 (N % 8 == 0)
+    float4 a = *reinterpret_cast<const float4 *>(part + i);
+    for (int s = 1; s < S; ++s) {
+        const float4 v = *reinterpret_cast<const float4 *>(part + (size_t)s * MN + i);
+        a.x += v.x;
+        a.y += v.y;
+        a.z += v.z;
+        a.w += v.w;
+    }
+    if constexpr (F16OUT) {
+        _Float16 *c = static_cast<_Float16 *>(C) + i;
+        c[0] = (_Float16)a.x;
+        c[1] = (_Float16)a.y;
+        c[2] = (_Float16)a.z;
+        c[3] = (_Float16)a.w;
+    } else {
+        *reinterpret_cast<float4 *>(static_cast<float *>(C) + i) = a;
+    }
+}
+
+struct Split {
+    int S, kps;
+    float *part;  // nullptr when S == 1
+};
+
 template <int GS, bool TILED>
 int launch_gs(st_context *ctx, const _Float16 *A, const uint32_t *qw, const uint16_t *sc, const uint32_t *qz, int zoff,
-              void *C, bool f16out, int M, int K, int N) {
+              void *C, bool f16out, int M, int K, int N, const Split &sp) {
     const int T = ((M + BM - 1) / BM) * ((N + BN - 1) / BN);
+    const dim3 grid(T * sp.S);
     if (f16out)
-        hipLaunchKernelGGL((gemm_kernel<GS, TILED, true>), dim3(T), dim3(kThreads), 0, ctx->stream, A, qw, sc, qz, zoff, C,
-                           M, K, N);
+        hipLaunchKernelGGL((gemm_kernel<GS, TILED, true>), grid, dim3(kThreads), 0, ctx->stream, A, qw, sc, qz, zoff, C, M,
+                           K, N, sp.kps, sp.part);
     else
-        hipLaunchKernelGGL((gemm_kernel<GS, TILED, false>), dim3(T), dim3(kThreads), 0, ctx->stream, A, qw, sc, qz, zoff,
-                           C, M, K, N);
-    return st::launch_check("gemm_kernel");
+        hipLaunchKernelGGL((gemm_kernel<GS, TILED, false>), grid, dim3(kThreads), 0, ctx->stream, A, qw, sc, qz, zoff, C,
+                           M, K, N, sp.kps, sp.part);
+    if (int rc = st::launch_check("gemm_kernel")) return rc;
+    if (sp.S > 1) {
+        const size_t MN = (size_t)M * N;
+        const dim3 rg((unsigned)((MN / 4 + 255) / 256));
+        if (f16out)
+            hipLaunchKernelGGL(splitk_reduce_kernel<true>, rg, dim3(256), 0, ctx->stream, sp.part, C, MN, sp.S);
+        else
+            hipLaunchKernelGGL(splitk_reduce_kernel<false>, rg, dim3(256), 0, ctx->stream, sp.part, C, MN, sp.S);
+        return st::launch_check("splitk_reduce_kernel");
+    }
+    return ST_OK;
 }
 
 template <bool TILED>
 int launch_tiled(st_context *ctx, const _Float16 *A, const uint32_t *qw, const uint16_t *sc, const uint32_t *qz, int zoff,
-                 void *C, bool f16out, int M, int K, int N, int gs) {
+                 void *C, bool f16out, int M, int K, int N, int gs, const Split &sp) {
     switch (gs) {
-        case 64: return launch_gs<64, TILED>(ctx, A, qw, sc, qz, zoff, C, f16out, M, K, N);
-        case 128: return launch_gs<128, TILED>(ctx, A, qw, sc, qz, zoff, C, f16out, M, K, N);
-        default: return launch_gs<256, TILED>(ctx, A, qw, sc, qz, zoff, C, f16out, M, K, N);
+        case 64: return launch_gs<64, TILED>(ctx, A, qw, sc, qz, zoff, C, f16out, M, K, N, sp);
+        case 128: return launch_gs<128, TILED>(ctx, A, qw, sc, qz, zoff, C, f16out, M, K, N, sp);
+        default: return launch_gs<256, TILED>(ctx, A, qw, sc, qz, zoff, C, f16out, M, K, N, sp);
     }
+}
+
+// Split K when the tiles alone fill at most half the CUs (the f32 partials
+// cost S * M * N * 8 bytes of extra traffic, which measured a loss at
+// configs[3] M = 512, 224 tiles): S splits of an even number of K tiles
+// each, as many as fill the workgroup slots (two per CU), at most 8, each at
+// least 4 K tiles, within the workspace left after A'.
+Split plan_split(st_context *ctx, int M, int K, int N, size_t ws_used) {
+    Split sp{1, K / KT, nullptr};
+    const int T = ((M + BM - 1) / BM) * ((N + BN - 1) / BN);
+    const int slots = 2 * ctx->num_cus;
+    const int ntiles = K / KT;
+    const char *no_split = std::getenv("ST_GEMM_NO_SPLIT");
+    if (2 * T > ctx->num_cus || ntiles < 8 || (no_split && *no_split && *no_split != '0')) return sp;
+    int S = std::min({8, (slots + T - 1) / T, ntiles / 4});
+    const size_t off = (ws_used + 255) & ~size_t(255);
+    while (S > 1 && off + (size_t)S * M * N * sizeof(float) > ctx->ws_bytes) --S;
+    if (S <= 1) return sp;
+    int kps = (ntiles + S - 1) / S;
+    kps += kps & 1;
+    sp.S = (ntiles + kps - 1) / kps;
+    sp.kps = kps;
+    sp.part = sp.S > 1 ? reinterpret_cast<float *>(reinterpret_cast<char *>(ctx->ws) + off) : nullptr;
+    if (sp.S == 1) sp.kps = ntiles;
+    return sp;
 }
 
 }  // namespace
@@ -414,6 +490,8 @@ extern "C" int st_gptq_i4_gemm(st_context *ctx, const uint16_t *a, const uint32_
     if (int rc = st::launch_check("prep_a_kernel")) return rc;
     const int zoff = (flags & ST_FLAG_ZEROS_PLUS_ONE) ? 1 : 0;
     const bool f16out = c_dtype == ST_F16;
-    if (flags & ST_FLAG_TILED) return launch_tiled<true>(ctx, A, qweight, scales, qzeros, zoff, c, f16out, M, K, N, group_size);
-    return launch_tiled<false>(ctx, A, qweight, scales, qzeros, zoff, c, f16out, M, K, N, group_size);
+    const Split sp = plan_split(ctx, M, K, N, need);
+    if (flags & ST_FLAG_TILED)
+        return launch_tiled<true>(ctx, A, qweight, scales, qzeros, zoff, c, f16out, M, K, N, group_size, sp);
+    return launch_tiled<false>(ctx, A, qweight, scales, qzeros, zoff, c, f16out, M, K, N, group_size, sp);
 }

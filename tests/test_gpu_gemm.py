@@ -159,3 +159,20 @@ def test_gemm_graph_replay_matches_eager(gpu, orc):
         assert torch.equal(out, eager), f"replay {i}"
         M.gptq_gemm(gpu, a, w.qweight, w.scales, eager, K, N, gs, w.qzeros, w.perm, w.flags)  # eager work between
         torch.cuda.synchronize()
+
+
+@pytest.mark.parametrize("gs", [64, 128, 256])
+def test_gemm_split_k_matches_unsplit(gpu, orc, gs, monkeypatch):
+    """Small grids split K across workgroups (f32 partials in the context
+    workspace, reduced in a fixed order): same result as one workgroup per
+    tile up to summation order, and the oracle's."""
+    Mr, K, N = 64, 4096, 264
+    c = orc.gptq_case(60 + gs, K, N, gs, zeros=True, act_order=True, M=Mr, x_dtype=np.float16)
+    w = up(gpu, c)
+    y_split = run_gemm(gpu, w, c["x"])
+    monkeypatch.setenv("ST_GEMM_NO_SPLIT", "1")
+    y_one = run_gemm(gpu, w, c["x"])
+    ref = orc.gptq_matvec_f64(c["x"], c["qweight"], c["scales"], K, N, gs, qzeros=c["qzeros"], g_idx=c["g_idx"])
+    e_s, e_o, e_so = orc.rel_l2(y_split, ref), orc.rel_l2(y_one, ref), orc.rel_l2(y_split, y_one)
+    print(f"split-K gs={gs}: split {e_s:.3e}, one {e_o:.3e}, split vs one {e_so:.3e}")
+    assert e_s < 5e-4 and e_o < 5e-4 and e_so < 1e-5
