@@ -373,6 +373,15 @@ def bench_stack(torch, dev, gpu, Mdl, gen, args):
                        "g": make_gptq(torch, dev, H, I, gen, gpu), "u": make_gptq(torch, dev, H, I, gen, gpu),
                        "d": make_gptq(torch, dev, I, H, gen, gpu)})
     lm = make_gptq(torch, dev, H, V, gen, gpu)
+    # q, k and v read the same x: one concatenated linear per layer (upload-time
+    # GptqWeight.cat; values unchanged), one launch instead of three
+    import shady_thinker_amd as sta
+
+    for w in layers:
+        parts = [sta.GptqWeight(w[n][0], w[n][1], None, None, H, d, GS, TF) for n, d in (("q", Q), ("k", KV), ("v", KV))]
+        qkv = sta.GptqWeight.cat(parts)
+        w["qkv"] = (qkv.qweight, qkv.scales)
+        del w["q"], w["k"], w["v"]
     per_layer = (decode_bytes(H, Q, 4, Q) + 2 * decode_bytes(H, KV, 4, KV) + decode_bytes(Q, H, 4, H) +
                  decode_bytes(H, 2 * I, 4, I) + decode_bytes(I, H, 4, H))
     out = {"layers": L, "weights_GB": None}
@@ -380,9 +389,7 @@ def bench_stack(torch, dev, gpu, Mdl, gen, args):
     for Mb in (1, 16):
         x = torch.randn(Mb, H, device=dev, generator=gen)
         attn = torch.randn(Mb, Q, device=dev, generator=gen)
-        yq = torch.empty(Mb, Q, device=dev)
-        yk = torch.empty(Mb, KV, device=dev)
-        yv = torch.empty(Mb, KV, device=dev)
+        yqkv = torch.empty(Mb, Q + 2 * KV, device=dev)
         yo = torch.empty(Mb, H, device=dev)
         h = torch.empty(Mb, I, device=dev)
         yd = torch.empty(Mb, H, device=dev)
@@ -390,9 +397,7 @@ def bench_stack(torch, dev, gpu, Mdl, gen, args):
 
         def token(i):
             for w in layers:
-                Mdl.gptq_matvec(gpu, "q_proj", x, w["q"][0], w["q"][1], yq, H, Q, GS, flags=TF)
-                Mdl.gptq_matvec(gpu, "k_proj", x, w["k"][0], w["k"][1], yk, H, KV, GS, flags=TF)
-                Mdl.gptq_matvec(gpu, "v_proj", x, w["v"][0], w["v"][1], yv, H, KV, GS, flags=TF)
+                Mdl.gptq_matvec(gpu, "qkv_proj", x, w["qkv"][0], w["qkv"][1], yqkv, H, Q + 2 * KV, GS, flags=TF)
                 Mdl.gptq_matvec(gpu, "o_proj", attn, w["o"][0], w["o"][1], yo, Q, H, GS, flags=TF)
                 Mdl.fused_gate_up_silu(gpu, x, w["g"][0], w["g"][1], w["u"][0], w["u"][1], h, H, I, GS, flags=TF)
                 Mdl.gptq_matvec(gpu, "down_proj", h, w["d"][0], w["d"][1], yd, I, H, GS, flags=TF)
@@ -407,7 +412,7 @@ def bench_stack(torch, dev, gpu, Mdl, gen, args):
         out[f"batch{Mb}"] = {"ms_per_token_step": round(ms, 4), "tokens_per_s": round(Mb / (ms * 1e-3), 1),
                              "GB/s": round(tok_bytes / (ms * 1e-3) / 1e9, 1),
                              "hbm_frac": round(tok_bytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
-                             "kernels_per_step": 6 * L + 1}
+                             "kernels_per_step": 4 * L + 1, "qkv": "one concatenated linear"}
     # Prefill of a 512-token prompt through the same weights with the GEMM
     # (f16 activations and outputs; q, k, v, o, gate, up, down per layer),
     # then the lm_head for the last token only, as a prefill does.
@@ -415,8 +420,7 @@ def bench_stack(torch, dev, gpu, Mdl, gen, args):
     xa = torch.randn(P, H, device=dev, generator=gen).half()
     aa = torch.randn(P, Q, device=dev, generator=gen).half()
     ha = torch.randn(P, I, device=dev, generator=gen).half()
-    cq = torch.empty(P, Q, device=dev, dtype=torch.float16)
-    ckv = torch.empty(P, KV, device=dev, dtype=torch.float16)
+    cq = torch.empty(P, Q + 2 * KV, device=dev, dtype=torch.float16)
     ch = torch.empty(P, H, device=dev, dtype=torch.float16)
     ci = torch.empty(P, I, device=dev, dtype=torch.float16)
     xl = torch.randn(1, H, device=dev, generator=gen)
@@ -424,9 +428,7 @@ def bench_stack(torch, dev, gpu, Mdl, gen, args):
 
     def prefill(i):
         for w in layers:
-            Mdl.gptq_gemm(gpu, xa, w["q"][0], w["q"][1], cq, H, Q, GS, None, None, TF)
-            Mdl.gptq_gemm(gpu, xa, w["k"][0], w["k"][1], ckv, H, KV, GS, None, None, TF)
-            Mdl.gptq_gemm(gpu, xa, w["v"][0], w["v"][1], ckv, H, KV, GS, None, None, TF)
+            Mdl.gptq_gemm(gpu, xa, w["qkv"][0], w["qkv"][1], cq, H, Q + 2 * KV, GS, None, None, TF)
             Mdl.gptq_gemm(gpu, aa, w["o"][0], w["o"][1], ch, Q, H, GS, None, None, TF)
             Mdl.gptq_gemm(gpu, xa, w["g"][0], w["g"][1], ci, H, I, GS, None, None, TF)
             Mdl.gptq_gemm(gpu, xa, w["u"][0], w["u"][1], ci, H, I, GS, None, None, TF)
@@ -436,7 +438,7 @@ def bench_stack(torch, dev, gpu, Mdl, gen, args):
     ms = Replayer(torch, prefill, 1).run(max(3, min(10, args.steps // 20)), 1)
     flops = 2.0 * P * L * (H * Q + 2 * H * KV + Q * H + 2 * H * I + I * H)
     out[f"prefill{P}"] = {"ms": round(ms, 3), "tokens_per_s": round(P / (ms * 1e-3), 1),
-                          "TFLOP/s": round(flops / (ms * 1e-3) / 1e12, 1), "gemm_calls": 7 * L}
+                          "TFLOP/s": round(flops / (ms * 1e-3) / 1e12, 1), "gemm_calls": 5 * L}
     out["weights_GB"] = round(wbytes / 1e9, 3)
     del layers, lm
     torch.cuda.empty_cache()

@@ -42,6 +42,12 @@ class QuantConfig:
             return cls.from_dict(json.load(f))
 
 
+def _torch():
+    import torch
+
+    return torch
+
+
 def _identity_groups(g_idx: np.ndarray, gs: int) -> bool:
     return bool(np.array_equal(g_idx, np.arange(g_idx.size, dtype=np.int64) // gs))
 
@@ -99,6 +105,38 @@ class GptqWeight:
             d_qw = d_t
             flags |= ST_FLAG_TILED
         return cls(d_qw, d_sc, d_qz, d_perm, K, N, group_size, flags)
+
+    @classmethod
+    def cat(cls, parts: list) -> "GptqWeight":
+        """Concatenate linears that share their input along N (q/k/v, or any
+        projections of the same x) into one: one launch instead of several,
+        outputs side by side in y. Dequantized values are unchanged: in the
+        tiled layout each 16-column tile is a contiguous run of words, so the
+        tiled buffers simply follow one another; in the [K/8, N] layout the
+        columns do. Needs equal K, group size, flags and act-order
+        permutation, qzeros on all parts or none, and N % 16 == 0 for all
+        parts but the last."""
+        torch = _torch()
+        p0 = parts[0]
+        for p in parts:
+            if (p.K, p.group_size, p.flags) != (p0.K, p0.group_size, p0.flags):
+                raise ValueError("GptqWeight.cat: parts differ in K, group size or flags")
+            if (p.qzeros is None) != (p0.qzeros is None) or (p.perm is None) != (p0.perm is None):
+                raise ValueError("GptqWeight.cat: qzeros / act-order present on some parts only")
+            if p.perm is not None and not torch.equal(p.perm, p0.perm):
+                raise ValueError("GptqWeight.cat: parts have different act-order permutations")
+        for p in parts[:-1]:
+            if p.N % 16:
+                raise ValueError(f"GptqWeight.cat: N={p.N} not a multiple of 16 before the last part")
+        if p0.tiled:
+            qw = torch.cat([p.qweight.reshape(-1) for p in parts])
+        else:
+            qw = torch.cat([p.qweight.reshape(p.K // 8, p.N) for p in parts], dim=1).contiguous()
+        sc = torch.cat([p.scales.reshape(p.K // p.group_size, p.N) for p in parts], dim=1).contiguous()
+        qz = None
+        if p0.qzeros is not None:
+            qz = torch.cat([p.qzeros.reshape(p.K // p.group_size, p.N // 8) for p in parts], dim=1).contiguous()
+        return cls(qw, sc, qz, p0.perm, p0.K, sum(p.N for p in parts), p0.group_size, p0.flags)
 
     @property
     def tiled(self) -> bool:

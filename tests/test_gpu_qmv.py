@@ -364,3 +364,20 @@ def test_graph_replay_matches_eager(gpu, orc):
         assert torch.equal(y2, y2_eager), rep
         M.gptq_matvec(gpu, "t", x, w.qweight, w.scales, y_eager, K, N, 128, flags=w.flags)  # eager work between
         torch.cuda.synchronize()
+
+
+@pytest.mark.parametrize("tiled", [True, False])
+def test_concatenated_linears_equal_separate_calls(gpu, orc, tiled):
+    """GptqWeight.cat (q/k/v sharing x): one matvec on the concatenation
+    returns the separate matvecs' outputs side by side, bit for bit."""
+    K = 1024
+    cs = [orc.gptq_case(70 + i, K, n, 128, zeros=True) for i, n in enumerate((256, 64, 72))]
+    ws = [up(gpu, c, tiled=tiled) for c in cs]
+    x = np.ascontiguousarray(orc.gptq_case(80, K, 16, 128, M=3)["x"])
+    sep = [run_matvec(gpu, w, x) for w in ws]
+    cat = sta.GptqWeight.cat(ws)
+    assert cat.N == 392
+    y = run_matvec(gpu, cat, x)
+    assert np.array_equal(y, np.concatenate(sep, axis=1))
+    with pytest.raises(ValueError):
+        sta.GptqWeight.cat([ws[2], ws[0]])  # N = 72 is not a multiple of 16 before the last part
