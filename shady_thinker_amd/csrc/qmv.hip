@@ -48,6 +48,9 @@ __global__ __launch_bounds__(256) void repack_kernel(const uint32_t *__restrict_
 int launch_i4(st_context *ctx, QmvParams &p, bool tiled, int nsrc, int xm) {
     p.units = p.K / p.gs;
     p.ntiles = (p.N + kTileN - 1) / kTileN;
+    // the tiled kernels address the weights with 32-bit buffer offsets
+    if (tiled && (size_t)p.ntiles * kTileN * p.K / 2 >= (size_t(1) << 31))
+        return st::fail(ST_ERR_SHAPE, "qmv: tiled weight of %d x %d exceeds 2 GiB", p.K, p.N);
     if (tiled) return p.perm ? dispatch<FMT_I4T, true>(ctx, p, nsrc, xm) : dispatch<FMT_I4T, false>(ctx, p, nsrc, xm);
     return p.perm ? dispatch<FMT_I4, true>(ctx, p, nsrc, xm) : dispatch<FMT_I4, false>(ctx, p, nsrc, xm);
 }
@@ -199,6 +202,8 @@ int st_int8_matvec(st_context *ctx, const void *x, int x_dtype, const int8_t *w,
     if (M < 1 || M > 32) return st::fail(ST_ERR_SHAPE, "st_int8_matvec: M=%d not in [1,32]", M);
     if (K <= 0 || K % 128) return st::fail(ST_ERR_SHAPE, "st_int8_matvec: K=%d not a positive multiple of 128", K);
     if (N <= 0 || N % 4) return st::fail(ST_ERR_SHAPE, "st_int8_matvec: N=%d not a positive multiple of 4", N);
+    if ((long long)N * K >= (1ll << 31))  // 32-bit buffer offsets
+        return st::fail(ST_ERR_SHAPE, "st_int8_matvec: weight of %d x %d exceeds 2 GiB", N, K);
     if (!st::aligned16(w) || !st::aligned16(x))
         return st::fail(ST_ERR_ALIGN, "st_int8_matvec: w and x must be 16-byte aligned");
     if (x_dtype != ST_F32 && x_dtype != ST_F16) return st::fail(ST_ERR_INVALID, "st_int8_matvec: x_dtype %d", x_dtype);

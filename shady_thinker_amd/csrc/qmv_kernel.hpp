@@ -57,6 +57,13 @@ typedef unsigned u32x4 __attribute__((ext_vector_type(4)));
 typedef unsigned u32x2 __attribute__((ext_vector_type(2)));
 
 constexpr int kTileN = 16;     // output columns per workgroup (per source)
+// Buffer resource word 3 for gfx9-class GPUs: raw (untyped) 32-bit data.
+constexpr int kBufWord3 = 0x00020000;
+// Tiled weights are read with buffer loads over a 2 GiB range; a ring slot
+// with nothing left to load uses this offset, which is out of range: the
+// load returns zeros without a memory access, and still counts as a load.
+constexpr unsigned kNoLoad = 0x80000000u;
+constexpr int kNt = 2;  // buffer-load cache policy: non-temporal (streamed once)
 constexpr int kMaxZeroUnits = 64;  // groups per wave whose zero points fit the LDS table
 
 enum Fmt { FMT_I4 = 0, FMT_I4T = 1, FMT_I8 = 2 };
@@ -81,6 +88,9 @@ struct Params {
     int chunk;     // groups staged per round trip
     int wave_lds;  // bytes of LDS per wave
     int nwaves;    // waves per workgroup (K is split among them)
+    int tpw;       // COOP: most tiles one workgroup owns (LDS zero table rows)
+    int grid;      // workgroups
+    int nstage;    // COOP: staging waves (they load no weights)
 };
 
 // silu(v) = v / (1 + exp(-v)) (fused_silu_gptq.wgsl:19-21), with the hardware
@@ -155,6 +165,33 @@ __device__ __forceinline__ void load_x16(const Params &p, int m, int k, float v[
     }
 }
 
+// Cross-lane max / sum over aligned groups of G lanes (G = 4, 8, 16) with
+// DPP row moves: quad_perm [1,0,3,2] and [2,3,0,1] combine a quad,
+// row_half_mirror pairs the two quads of 8 lanes, row_mirror the two halves
+// of 16.
+template <int CTRL>
+__device__ __forceinline__ int dpp_mov(int v) {
+    return __builtin_amdgcn_mov_dpp(v, CTRL, 0xF, 0xF, true);
+}
+template <int G>
+__device__ __forceinline__ float group_max(float v) {
+    static_assert(G == 4 || G == 8 || G == 16, "group of 4, 8 or 16 lanes");
+    v = fmaxf(v, __builtin_bit_cast(float, dpp_mov<0xB1>(__builtin_bit_cast(int, v))));
+    v = fmaxf(v, __builtin_bit_cast(float, dpp_mov<0x4E>(__builtin_bit_cast(int, v))));
+    if constexpr (G >= 8) v = fmaxf(v, __builtin_bit_cast(float, dpp_mov<0x141>(__builtin_bit_cast(int, v))));
+    if constexpr (G >= 16) v = fmaxf(v, __builtin_bit_cast(float, dpp_mov<0x140>(__builtin_bit_cast(int, v))));
+    return v;
+}
+template <int G>
+__device__ __forceinline__ int group_sum(int v) {
+    static_assert(G == 4 || G == 8 || G == 16, "group of 4, 8 or 16 lanes");
+    v += dpp_mov<0xB1>(v);
+    v += dpp_mov<0x4E>(v);
+    if constexpr (G >= 8) v += dpp_mov<0x141>(v);
+    if constexpr (G >= 16) v += dpp_mov<0x140>(v);
+    return v;
+}
+
 // dword of byte `bp` of a, b, c, d (in that order, low byte first).
 __device__ __forceinline__ unsigned pack4(unsigned a, unsigned b, unsigned c, unsigned d, int bp) {
     const unsigned sel = 0x0C0C0000u | ((4u + bp) << 8) | (unsigned)bp;
@@ -172,10 +209,15 @@ __device__ __forceinline__ void wait_vm_all() { __builtin_amdgcn_s_waitcnt(0x0F7
 // source (128 VGPRs each) or 8 for two. The fallback stages per wave, in
 // chunks, with 4 waves (256 VGPRs).
 template <int NSRC, bool COOP>
-constexpr int kMaxWavesFor = COOP ? (NSRC == 1 ? 16 : 8) : 4;
+constexpr int kMaxWavesFor = COOP ? (NSRC == 1 ? 16 : 12) : 4;
+constexpr int kMaxTilesPerWg = 4;  // COOP: tiles one workgroup may own
+// COOP: ring slots issued before the staging barrier (or, per-wave staging,
+// before the staging): more would keep the barrier waiting for waves stalled
+// at a full memory queue; fewer delay the weight stream
+constexpr int kRingBeforeBarrier = 2;
 
-constexpr int kCoopRounds = 2;  // x staging rounds per lane in COOP kernels (bounds M * K)
-constexpr int kScaleUnits = 8;  // groups per wave covered by the COOP scale block (one load per source)
+constexpr int kCoopRounds = 4;  // x staging rounds per staging wave in COOP kernels
+constexpr int kScaleUnits = 16;  // groups per wave covered by the COOP scale block (two loads per source)
 
 // Prefetch ring depth: the registers of weights in flight per lane, about 24
 // under a 128-VGPR budget (16-wave workgroups) and 40 for the dual kernel
@@ -190,10 +232,14 @@ constexpr int ring_depth() {
     return (budget / RPU) < 2 ? 2 : ((budget / RPU) > 6 ? 6 : (budget / RPU));
 }
 
-template <int FMT, int NSRC, int XM, int MB, int SPU, bool PERM, bool COOP>
-__global__ __launch_bounds__((64 * kMaxWavesFor<NSRC, COOP>)) void qmv_kernel(Params p) {
+// CM (staging mode): 0 = per-wave chunks (fallback), 1 = cooperative with
+// staging waves, 2 = cooperative, each wave staging its own groups.
+template <int FMT, int NSRC, int XM, int MB, int SPU, bool PERM, int CM>
+__global__ __launch_bounds__((64 * kMaxWavesFor<NSRC, (CM != 0)>)) void qmv_kernel(Params p) {
+    constexpr bool COOP = CM != 0;
     extern __shared__ __align__(16) unsigned char smem[];
     constexpr int D = ring_depth<FMT, NSRC, SPU, COOP>();
+    constexpr int DPRE = kRingBeforeBarrier < D ? kRingBeforeBarrier : D;  // COOP: slots before the barrier
     constexpr int IPU = 4 * SPU;                              // 16-k items per group and token
     constexpr int WPU = (FMT == FMT_I8) ? 4 * SPU : 2 * SPU;  // weight dwords per lane per group
     // staging rounds per lane: per-wave chunk (fallback) or whole slice (COOP)
@@ -210,19 +256,40 @@ __global__ __launch_bounds__((64 * kMaxWavesFor<NSRC, COOP>)) void qmv_kernel(Pa
 
     // Workgroups are dealt to the 8 XCDs round-robin; give each XCD a
     // contiguous run of tiles so neighbouring tiles share L2 lines.
+    // COOP: workgroup r owns tiles [t0, t0 + TB) (TB >= 1; more than one when
+    // N has more tiles than the grid has workgroups, so x is staged once for
+    // them all); compute wave cw serves tile t0 + cw % TB, K slice cw / TB.
+    // Fallback: one tile per workgroup.
     const int b = blockIdx.x;
-    const int tile = (p.ntiles % 8 == 0) ? (b % 8) * (p.ntiles / 8) + b / 8 : b;
+    const int G = gridDim.x;
+    const int r_wg = (G % 8 == 0) ? (b % 8) * (G / 8) + b / 8 : b;
+    // (32-bit divisions: the host keeps ntiles * G below 2^31 when G < ntiles)
+    const bool multi = COOP && G != p.ntiles;
+    const int t0 = multi ? (int)((unsigned)(r_wg * p.ntiles) / (unsigned)G) : r_wg;
+    const int TB = multi ? (int)((unsigned)((r_wg + 1) * p.ntiles) / (unsigned)G) - t0 : 1;
+    // COOP: waves [0, NS) only stage x (at most RMAX rounds of 64 items
+    // each); the others split the tiles' K. Fallback: every wave stages its
+    // own chunk.
+    constexpr bool PW = CM == 2;  // per-wave staging of the wave's own groups, no staging waves
+    const int CH = COOP ? p.units : p.chunk;  // units the A region holds
+    const int NS = (COOP && !PW) ? p.nstage : 0;  // host: ceil(items / 64 RMAX) <= NS <= NW - TB
+    const int cw = wave - NS;             // compute-wave index (< 0: a staging wave)
+    const int WPT = (NW - NS) / TB;       // compute waves per tile; the rest idle
+    const int tj = cw >= 0 ? cw % TB : 0;  // tile slot of this wave
+    const int ks = cw >= 0 ? cw / TB : WPT;  // K slice of this wave (WPT: none)
+    const int tile = t0 + tj;
     const int n0 = tile * kTileN;
     const int ncol = min(n0 + c, N - 1);  // clamped column this lane loads
 
-    const int u0 = (int)((long long)wave * p.units / NW);
-    const int u1 = (int)((long long)(wave + 1) * p.units / NW);
+    const int u0 = ks < WPT ? (int)((unsigned)(ks * p.units) / (unsigned)WPT) : 0;
+    const int u1 = ks < WPT ? (int)((unsigned)((ks + 1) * p.units) / (unsigned)WPT) : 0;
+    const int SW = PW ? u1 - u0 : CH;  // units staged by this wave's staging rounds
+    const int items = M * SW * IPU;
 
     // LDS: A operands [unit][step][mb][q][row] (16 B each), per (unit, token)
     // 2^-e, -H, -L (sum(X) = H*65536 + L), zero points [unit][src][column].
     // COOP: one region for the workgroup, units = all groups; fallback: one
     // region per wave, units = one chunk (zero table: the wave's groups).
-    const int CH = COOP ? p.units : p.chunk;  // units staged at once
     const int ZU = COOP ? p.units : (u1 - u0);
     unsigned char *region = smem + (COOP ? 0 : (size_t)wave * p.wave_lds);
     u32x4 *abuf = reinterpret_cast<u32x4 *>(region);
@@ -232,7 +299,7 @@ __global__ __launch_bounds__((64 * kMaxWavesFor<NSRC, COOP>)) void qmv_kernel(Pa
     int *s_nl = s_nh + CH * M;
     unsigned char *s_z = reinterpret_cast<unsigned char *>(s_nl + CH * M);
     const int zbase = COOP ? 0 : u0;  // unit index of s_z row 0
-    // COOP scale table: [wave][src][group - u0 (< kScaleUnits)][16 columns], after the reduction area
+    // COOP scale table: [wave][src][group - u0 (< kScaleUnits = 16)][16 columns], after the reduction area
     uint16_t *s_sc = reinterpret_cast<uint16_t *>(smem + (size_t)p.wave_lds + (size_t)NW * NSRC * MB * 64 * sizeof(float));
 
     // ------------------------------------------- zero points (before all loads)
@@ -241,11 +308,13 @@ __global__ __launch_bounds__((64 * kMaxWavesFor<NSRC, COOP>)) void qmv_kernel(Pa
     for (int src = 0; src < NSRC; ++src) have_z[src] = FMT != FMT_I8 && p.qz[src] != nullptr;
     if constexpr (FMT != FMT_I8) {
         if (have_z[0]) {
-            const int nz = ZU * NSRC * 16;
-            const int first = COOP ? tid : lane, stride = COOP ? 64 * NW : 64;
-            for (int i = first; i < nz; i += stride) {
-                const int col = i & 15, src = (i >> 4) % NSRC, uz = i / (16 * NSRC);
-                const int zc = min(n0 + col, N - 1);
+            // [tile slot][unit][src][column]; PW: each wave its own tile and groups
+            const int nz = PW ? (u1 - u0) * NSRC * 16 : TB * ZU * NSRC * 16;
+            const int first = (COOP && !PW) ? tid : lane, stride = (COOP && !PW) ? 64 * NW : 64;
+            for (int i0 = first; i0 < nz; i0 += stride) {
+                const int i = PW ? (tj * ZU + u0) * NSRC * 16 + i0 : i0;
+                const int col = i & 15, src = (i >> 4) % NSRC, uz = (i / (16 * NSRC)) % ZU, tz = i / (16 * NSRC * ZU);
+                const int zc = min((t0 + tz) * kTileN + col, N - 1);
                 const unsigned w = p.qz[src][(size_t)(zbase + uz) * (N >> 3) + (zc >> 3)];
                 s_z[i] = (unsigned char)(((w >> (4 * (zc & 7))) & 0xF) + p.zoff);
             }
@@ -258,7 +327,15 @@ __global__ __launch_bounds__((64 * kMaxWavesFor<NSRC, COOP>)) void qmv_kernel(Pa
         unsigned w[NSRC][WPU];
         unsigned short s[NSRC];
     };
-    auto load_unit = [&](Unit &U, int u) {
+    // tiled layout: one buffer resource per source (separate variables: an
+    // array of resources loses the kernel's host stub)
+    const __amdgpu_buffer_rsrc_t rq0 = __builtin_amdgcn_make_buffer_rsrc((void *)p.qw[0], (short)0, 0x7FFFFFFF, kBufWord3);
+    const __amdgpu_buffer_rsrc_t rq1 =
+        __builtin_amdgcn_make_buffer_rsrc((void *)p.qw[NSRC - 1], (short)0, 0x7FFFFFFF, kBufWord3);
+    const __amdgpu_buffer_rsrc_t rw8 = __builtin_amdgcn_make_buffer_rsrc((void *)p.w8, (short)0, 0x7FFFFFFF, kBufWord3);
+    // !live: an empty ring slot (u is then a clamped valid group; the tiled
+    // layout skips the memory access, the others read that group again)
+    auto load_unit = [&](Unit &U, int u, bool live) {
 #pragma unroll
         for (int src = 0; src < NSRC; ++src) {
             if constexpr (FMT == FMT_I4) {
@@ -270,15 +347,16 @@ __global__ __launch_bounds__((64 * kMaxWavesFor<NSRC, COOP>)) void qmv_kernel(Pa
                         U.w[src][2 * st + h] = __builtin_nontemporal_load(p.qw[src] + pr * N + ncol);
                     }
             } else if constexpr (FMT == FMT_I4T) {
-                const uint32_t *base = p.qw[src] + (((size_t)tile * p.units + u) * 64 + lane) * WPU;
+                const unsigned off = live ? (unsigned)(((tile * p.units + u) * 64 + lane) * WPU * 4) : kNoLoad;
+                const __amdgpu_buffer_rsrc_t rq = src == 0 ? rq0 : rq1;
                 if constexpr (WPU == 2) {
-                    const u32x2 t = __builtin_nontemporal_load(reinterpret_cast<const u32x2 *>(base));
+                    const u32x2 t = __builtin_amdgcn_raw_buffer_load_b64(rq, off, 0, kNt);
                     U.w[src][0] = t.x;
                     U.w[src][1] = t.y;
                 } else {
 #pragma unroll
                     for (int j = 0; j < WPU; j += 4) {
-                        const u32x4 t = __builtin_nontemporal_load(reinterpret_cast<const u32x4 *>(base + j));
+                        const u32x4 t = __builtin_amdgcn_raw_buffer_load_b128(rq, off + j * 4, 0, kNt);
                         U.w[src][j] = t.x;
                         U.w[src][j + 1] = t.y;
                         U.w[src][j + 2] = t.z;
@@ -286,10 +364,10 @@ __global__ __launch_bounds__((64 * kMaxWavesFor<NSRC, COOP>)) void qmv_kernel(Pa
                     }
                 }
             } else {
-                const int8_t *row = p.w8 + (size_t)ncol * K + (size_t)u * 128 + 16 * q;
+                const unsigned off = live ? (unsigned)(ncol * K + u * 128 + 16 * q) : kNoLoad;
 #pragma unroll
                 for (int st = 0; st < SPU; ++st) {
-                    const u32x4 t = __builtin_nontemporal_load(reinterpret_cast<const u32x4 *>(row + 64 * st));
+                    const u32x4 t = __builtin_amdgcn_raw_buffer_load_b128(rw8, off + 64 * st, 0, kNt);
                     U.w[src][4 * st] = t.x;
                     U.w[src][4 * st + 1] = t.y;
                     U.w[src][4 * st + 2] = t.z;
@@ -303,25 +381,32 @@ __global__ __launch_bounds__((64 * kMaxWavesFor<NSRC, COOP>)) void qmv_kernel(Pa
     Unit ring[D];
 
     // ------------------------------------------------------ x staging
-    // Round r covers items i = r * span + t (t = thread index in the staging
-    // group: the workgroup for COOP, the wave otherwise). Item i is token
-    // m = i / (CH*IPU), group cs + (i % (CH*IPU)) / IPU, 16 k of it. Every
-    // thread loads in every round (absent items read a clamped valid address).
+    // Round r of wave w covers the 64 items of row w + NS r in COOP kernels
+    // (waves [0, NS) stage everything, the others only stream weights), of
+    // row r in the fallback (each wave its own chunk); item i = row * 64 +
+    // lane is token m = i / (CH*IPU), group cs + (i % (CH*IPU)) / IPU, 16 k of
+    // it. Every lane of a wave with items in a round loads (absent items read
+    // a clamped valid address).
     const int span = COOP ? 64 * NW : 64;
     const int tt = COOP ? tid : lane;
-    const int uend = COOP ? p.units : u1;  // staged groups end here
+    const int rstep = (COOP && !PW) ? NS : 1;  // row stride between rounds
+    const int wave0 = (COOP && !PW) ? wave : 0;  // row of round 0
+    const int uend = (COOP && !PW) ? p.units : u1;  // staged groups end here
     float xv[RMAX][16];
-    const int items = M * CH * IPU;
     // A wave with no item in a round skips it (loads and work): the branch
     // is uniform per wave and the same condition guards the loads and their
     // only consumer, stage().
-    const int wfirst = COOP ? wave * 64 : 0;
     auto xload = [&](int cs) {
 #pragma unroll
         for (int r = 0; r < RMAX; ++r) {
-            if (r * span + wfirst >= items) continue;
-            const int i = min(r * span + tt, items - 1);
-            const int m = i / (CH * IPU), w = i - m * (CH * IPU);
+            const int row = wave0 + r * rstep;
+            if (row * 64 >= items) continue;
+            const int i = min(row * 64 + lane, items - 1);
+            int m = 0, w = i;
+            if (M > 1) {
+                m = i / (SW * IPU);
+                w = i - m * (SW * IPU);
+            }
             const int u = min(cs + w / IPU, uend - 1);
             load_x16<XM, PERM>(p, m, u * p.gs + 16 * (w % IPU), xv[r]);
         }
@@ -329,10 +414,16 @@ __global__ __launch_bounds__((64 * kMaxWavesFor<NSRC, COOP>)) void qmv_kernel(Pa
     auto stage = [&](int cs) {
 #pragma unroll
         for (int r = 0; r < RMAX; ++r) {
-            if (r * span + wfirst >= items) continue;  // uniform per wave
-            const int i = r * span + tt;
-            const int m = i / (CH * IPU), w = i - m * (CH * IPU);
+            const int row = wave0 + r * rstep;
+            if (row * 64 >= items) continue;  // uniform per wave
+            const int i = row * 64 + lane;
+            int m = 0, w = i;
+            if (M > 1) {
+                m = i / (SW * IPU);
+                w = i - m * (SW * IPU);
+            }
             const int ui = w / IPU, ii = w % IPU;
+            const int ua = COOP ? cs + ui : ui;  // A-region unit (COOP: the group itself)
             const bool ok = i < items && cs + ui < uend;
             float amax = 0.0f, nf = 0.0f;
 #pragma unroll
@@ -343,55 +434,65 @@ __global__ __launch_bounds__((64 * kMaxWavesFor<NSRC, COOP>)) void qmv_kernel(Pa
             // a non-finite x poisons its group: amax = inf -> 2^-e = NaN -> y = NaN
             amax = (nf == nf) ? amax : INFINITY;
             if (!ok) amax = 0.0f;
-#pragma unroll
-            for (int o = 1; o < IPU; o <<= 1) amax = fmaxf(amax, __shfl_xor(amax, o));
+            amax = group_max<IPU>(amax);
             int e = 0;
             float em = 1.0f;
             if (amax == INFINITY) {
                 em = __builtin_nanf("");
             } else if (amax > 0.0f) {
-                e = 21 - ilogbf(amax);
+                // amax = f 2^fe, f in [0.5, 1): floor(log2 amax) = fe - 1
+                e = 22 - __builtin_amdgcn_frexp_expf(amax);
                 e = e > 100 ? 100 : (e < -100 ? -100 : e);
-                em = ldexpf(1.0f, -e);
+                em = __builtin_amdgcn_ldexpf(1.0f, -e);
             }
-            const float sc2 = ldexpf(1.0f, e);
-            int X[16];
-            int sum = 0;
+            const float sc2 = __builtin_amdgcn_ldexpf(1.0f, e);
+            // X = round(x 2^e) in one FMA: |x 2^e| < 2^22 when amax is finite
+            // (otherwise the group is NaN anyway), so v = x 2^e + 1.5 * 2^23
+            // lies in [2^23, 2^24), where the floats are the integers: the FMA
+            // rounds x 2^e to the nearest integer (ties to even) and bits(v) =
+            // 0x4B400000 + X.
+            unsigned Z[16];
+            unsigned ysum = 0;
 #pragma unroll
             for (int j = 0; j < 16; ++j) {
-                // |x| 2^e < 2^22 when amax is finite; otherwise the group is NaN anyway
-                X[j] = __float2int_rn(xv[r][j] * sc2);
-                sum += X[j];
+                const unsigned y = __builtin_bit_cast(unsigned, fmaf(xv[r][j], sc2, 12582912.0f));
+                ysum += y;
+                // Z = Y + 0xC08080 = X + 0x8080 (mod 2^24): byte 2 of Z is the
+                // limb L2 = byte 2 of X + 32896, bytes 1 and 0 of Z are L1 =
+                // byte 1 of X + 128 and L0 = byte 0 of X, each plus 128 (mod 256)
+                Z[j] = y + 0xC08080u;
             }
-#pragma unroll
-            for (int o = 1; o < IPU; o <<= 1) sum += __shfl_xor(sum, o);
+            int sum = group_sum<IPU>((int)(ysum - 16u * 0x4B400000u));
             if (ok) {
                 // Operand byte J holds element koff(J) (GPTQ nibble order) or J.
-                // Limb bytes: L0 = byte 0 of X, L1 = byte 1 of X + 128,
-                // L2 = byte 2 of X + 32896 (balanced base-256 digits).
                 u32x4 L2v, L1v, L0v;
 #pragma unroll
                 for (int rr = 0; rr < 4; ++rr) {
                     constexpr bool nat = FMT == FMT_I8;
-                    const unsigned a = (unsigned)X[nat ? 4 * rr : i4_koff(4 * rr)];
-                    const unsigned bb = (unsigned)X[nat ? 4 * rr + 1 : i4_koff(4 * rr + 1)];
-                    const unsigned cc = (unsigned)X[nat ? 4 * rr + 2 : i4_koff(4 * rr + 2)];
-                    const unsigned dd = (unsigned)X[nat ? 4 * rr + 3 : i4_koff(4 * rr + 3)];
-                    L2v[rr] = pack4(a + 32896u, bb + 32896u, cc + 32896u, dd + 32896u, 2);
-                    L1v[rr] = pack4(a + 128u, bb + 128u, cc + 128u, dd + 128u, 1);
-                    L0v[rr] = pack4(a, bb, cc, dd, 0);
+                    const unsigned a = Z[nat ? 4 * rr : i4_koff(4 * rr)];
+                    const unsigned bb = Z[nat ? 4 * rr + 1 : i4_koff(4 * rr + 1)];
+                    const unsigned cc = Z[nat ? 4 * rr + 2 : i4_koff(4 * rr + 2)];
+                    const unsigned dd = Z[nat ? 4 * rr + 3 : i4_koff(4 * rr + 3)];
+                    // [a0 b0 a1 b1], [c0 d0 c1 d1], [a2 b2 -- --], [c2 d2 -- --]
+                    const unsigned ab01 = __builtin_amdgcn_perm(bb, a, 0x05010400u);
+                    const unsigned cd01 = __builtin_amdgcn_perm(dd, cc, 0x05010400u);
+                    const unsigned ab2 = __builtin_amdgcn_perm(bb, a, 0x0C0C0602u);
+                    const unsigned cd2 = __builtin_amdgcn_perm(dd, cc, 0x0C0C0602u);
+                    L2v[rr] = __builtin_amdgcn_perm(cd2, ab2, 0x05040100u);
+                    L1v[rr] = __builtin_amdgcn_perm(cd01, ab01, 0x07060302u) ^ 0x80808080u;
+                    L0v[rr] = __builtin_amdgcn_perm(cd01, ab01, 0x05040100u) ^ 0x80808080u;
                 }
                 const int st = ii >> 2, qq = ii & 3;
-                u32x4 *dst = abuf + (((size_t)(ui * SPU + st) * MB + (m >> 2)) * 4 + qq) * RB + 4 * (m & 3);
+                u32x4 *dst = abuf + (((size_t)(ua * SPU + st) * MB + (m >> 2)) * 4 + qq) * RB + 4 * (m & 3);
                 dst[0] = L2v;
                 dst[1] = L1v;
                 dst[2] = L0v;
                 dst[3] = u32x4{0, 0, 0, 0};  // row 4t+3 (see the zero fill below)
                 if (ii == 0) {
                     const int h = (sum + 32768) >> 16;
-                    s_em[ui * M + m] = em;
-                    s_nh[ui * M + m] = -h;
-                    s_nl[ui * M + m] = -(sum - (h << 16));
+                    s_em[ua * M + m] = em;
+                    s_nh[ua * M + m] = -h;
+                    s_nl[ua * M + m] = -(sum - (h << 16));
                 }
             }
         }
@@ -457,9 +558,9 @@ __global__ __launch_bounds__((64 * kMaxWavesFor<NSRC, COOP>)) void qmv_kernel(Pa
                 if constexpr (FMT == FMT_I8) {
                     f = em;
                 } else {
-                    const uint16_t sh = COOP ? s_sc[(wave * NSRC + src) * 128 + (u - u0) * 16 + c] : U.s[src];
+                    const uint16_t sh = COOP ? s_sc[(wave * NSRC + src) * 256 + (u - u0) * 16 + c] : U.s[src];
                     f = (float)__builtin_bit_cast(_Float16, sh) * em;
-                    z = have_z[src] ? (int)s_z[((u - zbase) * NSRC + src) * 16 + c] : 8;
+                    z = have_z[src] ? (int)s_z[((tj * ZU + u - zbase) * NSRC + src) * 16 + c] : 8;
                 }
                 const int hi = S.x + __mul24(z, nh);
                 const int lo = (S.y << 8) + S.z + __mul24(z, nl);
@@ -478,34 +579,71 @@ __global__ __launch_bounds__((64 * kMaxWavesFor<NSRC, COOP>)) void qmv_kernel(Pa
         stage(u);
     };
 
-    // x first (loads complete in issue order, so the x slice must not queue
-    // behind the weight ring), then the ring, all unconditionally.
-    const int cs0 = COOP ? 0 : u0;
-    if (COOP || u0 < u1) xload(cs0);
+    // COOP: the staging waves load x, wait for it and stage it; they issue no
+    // weight load, so neither x nor the staging queues behind the weight
+    // stream at the CU's memory port, and the other waves start streaming at
+    // once. Nothing is in flight across the branch. Fallback: x first (loads complete in issue order),
+    // then the ring, then the staging.
+    const int cs0 = (COOP && !PW) ? 0 : u0;
+    if (COOP && !PW && wave < NS) {
+        xload(cs0);
+        wait_vm_all();
+        stage(cs0);
+    }
+    if (PW) xload(cs0);  // (a wave without groups has no items: uniform skip inside)
+    if (!COOP && u0 < u1) xload(cs0);
     // COOP GPTQ: the scales of the wave's (at most kScaleUnits) groups for
-    // the tile's 16 columns in one 4-byte load per lane and source (lane l:
-    // group u0 + l / 8, columns 2 (l % 8) and +1), instead of one 2-byte
-    // load per group in the ring: half the ring's load instructions. Issued
-    // after x and before the ring, so waiting for them never waits for the
-    // ring; parked in LDS after the staging.
-    unsigned scw[NSRC];
+    // the tile's 16 columns in two 4-byte loads per lane and source (lane l,
+    // load h: group u0 + 8h + l / 8, columns 2 (l % 8) and +1; lanes past the
+    // wave's groups load nothing), instead of one 2-byte load per group in
+    // the ring. Issued before the ring, so waiting for them never waits for
+    // the ring; parked in LDS before the barrier.
+    unsigned scw[NSRC][2];
     if constexpr (SCB) {
-        const int ul = min(u0 + (lane >> 3), max(u1, 1) - 1);
+        const __amdgpu_buffer_rsrc_t rs0 = __builtin_amdgcn_make_buffer_rsrc((void *)p.sc[0], (short)0, 0x7FFFFFFF, kBufWord3);
+        const __amdgpu_buffer_rsrc_t rs1 =
+            __builtin_amdgcn_make_buffer_rsrc((void *)p.sc[NSRC - 1], (short)0, 0x7FFFFFFF, kBufWord3);
         const int cl = min(n0 + 2 * (lane & 7), N - 2);
 #pragma unroll
+        for (int h = 0; h < 2; ++h) {
+            const int ug = u0 + 8 * h + (lane >> 3);
+            const unsigned off = ug < u1 ? (unsigned)(((size_t)ug * N + cl) * 2) : kNoLoad;
+#pragma unroll
+            for (int src = 0; src < NSRC; ++src)
+                scw[src][h] = __builtin_amdgcn_raw_buffer_load_b32(src == 0 ? rs0 : rs1, off, 0, 0);
+        }
+    }
+    // COOP: issued by every wave (waves without groups issue only empty
+    // slots, which access no memory): a branch here would make the compiler
+    // wait for the whole ring wherever it waits for the scales.
+    if (COOP || u0 < u1) {
+#pragma unroll
+        for (int d = 0; d < (COOP ? DPRE : D); ++d)
+            load_unit(ring[d], min(u0 + d, max(u1 - 1, 0)), u0 + d < u1);
+    }
+    if (!COOP && u0 < u1) stage(cs0);
+    if constexpr (PW) {
+        stage(cs0);
+#pragma unroll
+        for (int d = DPRE; d < D; ++d) load_unit(ring[d], min(u0 + d, max(u1 - 1, 0)), u0 + d < u1);
+    } else if constexpr (COOP) {
+        // The staged x (and the zero table) are complete: this wave's LDS
+        // writes have landed (lgkmcnt(0)) and every wave has arrived. Not
+        // __syncthreads(): its release fence also waits for every load in
+        // flight (vmcnt(0)), i.e. for the ring. The asm's memory clobber
+        // keeps the compiler from moving LDS accesses across it.
+        asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+        // the rest of the ring, after the barrier: issuing it can stall while
+        // the CU's memory queue is full, and that must not hold up the barrier
+#pragma unroll
+        for (int d = DPRE; d < D; ++d) load_unit(ring[d], min(u0 + d, max(u1 - 1, 0)), u0 + d < u1);
+    }
+    if constexpr (SCB) {  // the wave's own scale table: no barrier needed
+#pragma unroll
         for (int src = 0; src < NSRC; ++src)
-            scw[src] = *reinterpret_cast<const unsigned *>(p.sc[src] + (size_t)ul * N + cl);
-    }
-    if (u0 < u1) {
 #pragma unroll
-        for (int d = 0; d < D; ++d) load_unit(ring[d], min(u0 + d, u1 - 1));
+            for (int h = 0; h < 2; ++h) reinterpret_cast<unsigned *>(s_sc)[(wave * NSRC + src) * 128 + h * 64 + lane] = scw[src][h];
     }
-    if (COOP || u0 < u1) stage(cs0);
-    if constexpr (SCB) {
-#pragma unroll
-        for (int src = 0; src < NSRC; ++src) reinterpret_cast<unsigned *>(s_sc)[(wave * NSRC + src) * 64 + lane] = scw[src];
-    }
-    if constexpr (COOP) __syncthreads();
     if (u0 < u1) {
         int ui = COOP ? u0 : 0;  // A-buffer index of the current group
         int base = u0;
@@ -519,7 +657,7 @@ __global__ __launch_bounds__((64 * kMaxWavesFor<NSRC, COOP>)) void qmv_kernel(Pa
                 }
                 compute(ring[d], u, ui);
                 ++ui;
-                load_unit(ring[d], min(u + D, u1 - 1));
+                load_unit(ring[d], min(u + D, u1 - 1), u + D < u1);
             }
         }
 #pragma unroll
@@ -543,8 +681,8 @@ __global__ __launch_bounds__((64 * kMaxWavesFor<NSRC, COOP>)) void qmv_kernel(Pa
 #pragma unroll
         for (int mb = 0; mb < MB; ++mb) red[((wave * NSRC + src) * MB + mb) * 64 + lane] = tot[src][mb];
     __syncthreads();
-    if (wave != 0) return;
-    const int n = n0 + c;
+    if (wave >= TB) return;  // wave j (< TB) sums the K slices of tile t0 + j, in slice order
+    const int n = (t0 + wave) * kTileN + c;  // column of tile t0 + wave
 #pragma unroll
     for (int mb = 0; mb < MB; ++mb) {
         const int m = mb * 4 + q;
@@ -552,7 +690,7 @@ __global__ __launch_bounds__((64 * kMaxWavesFor<NSRC, COOP>)) void qmv_kernel(Pa
 #pragma unroll
         for (int src = 0; src < NSRC; ++src) {
             float a = 0.0f;
-            for (int w = 0; w < NW; ++w) a += red[((w * NSRC + src) * MB + mb) * 64 + lane];
+            for (int w = wave; w < TB * WPT; w += TB) a += red[(((NS + w) * NSRC + src) * MB + mb) * 64 + lane];
             v[src] = a;
         }
         if (m >= M || n >= N) continue;
@@ -578,12 +716,12 @@ inline size_t unit_bytes(const Params &p) {
     return (size_t)SPU * MB * 4 * p.rb * 16 + (size_t)p.M * 12 + (FMT == FMT_I8 ? 0 : (size_t)NSRC * 16);
 }
 
-template <int FMT, int NSRC, int XM, int MB, int SPU, bool PERM, bool COOP>
+template <int FMT, int NSRC, int XM, int MB, int SPU, bool PERM, int CM>
 int launch_kernel(st_context *ctx, Params &p, size_t lds) {
-    auto kern = qmv_kernel<FMT, NSRC, XM, MB, SPU, PERM, COOP>;
+    auto kern = qmv_kernel<FMT, NSRC, XM, MB, SPU, PERM, CM>;
     if (lds > 64 * 1024)
         ST_HIP(hipFuncSetAttribute((const void *)kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds));
-    hipLaunchKernelGGL(kern, dim3(p.ntiles), dim3(64 * p.nwaves), lds, ctx->stream, p);
+    hipLaunchKernelGGL(kern, dim3(p.grid), dim3(64 * p.nwaves), lds, ctx->stream, p);
     return launch_check("qmv_kernel");
 }
 
@@ -599,27 +737,81 @@ int launch_t(st_context *ctx, Params &p) {
     const int want = (ctx->num_cus * 16) / std::max(1, p.ntiles);
     if constexpr (MB == 1 && FMT != FMT_I4) {
         constexpr int NWX = kMaxWavesFor<NSRC, true>;
-        int nw = want >= 16 ? 16 : (want >= 8 ? 8 : 4);
-        nw = std::max(4, std::min({nw, NWX, std::max(4, p.units)}));
-        nw = std::max(4, std::min(NWX, env_int("ST_QMV_WAVES", nw)));
-        // GPTQ: at most kScaleUnits groups per wave (the scale block)
-        if (FMT != FMT_I8)
-            while ((p.units + nw - 1) / nw > kScaleUnits && nw < NWX) nw *= 2;
-        const bool scb_ok = FMT == FMT_I8 || (p.units + nw - 1) / nw <= kScaleUnits;
-        const size_t ub = unit_bytes<FMT, NSRC, MB, SPU>(p);
-        const size_t lds = ((ub * p.units + 15) & ~size_t(15)) + (size_t)nw * NSRC * MB * 64 * sizeof(float) +
-                           (FMT != FMT_I8 ? (size_t)nw * NSRC * 64 * sizeof(unsigned) : 0);
         const long long items = (long long)p.M * p.units * IPU;
-        if (scb_ok && lds <= kCoopLdsBudget && items <= (long long)kCoopRounds * 64 * nw &&
-            !env_int("ST_QMV_NO_COOP", 0)) {
+        // launches the COOP kernel with this shape if it fits; -1 = it does not.
+        // Staging waves: as many as one round each needs (staging latency),
+        // fewer (up to kCoopRounds rounds each) when K needs the waves.
+        auto try_coop = [&](int nw, int tpw, int grid) -> int {
+            const size_t ub = unit_bytes<FMT, NSRC, MB, SPU>(p);
+            const size_t region =
+                (ub * p.units + (FMT != FMT_I8 ? (size_t)(tpw - 1) * p.units * NSRC * 16 : 0) + 15) & ~size_t(15);
+            const size_t lds = region + (size_t)nw * NSRC * MB * 64 * sizeof(float) +
+                               (FMT != FMT_I8 ? (size_t)nw * NSRC * 128 * sizeof(unsigned) : 0);
+            if (lds > kCoopLdsBudget) return -1;
             p.nwaves = nw;
-            p.wave_lds = (int)((ub * p.units + 15) & ~size_t(15));
-            return launch_kernel<FMT, NSRC, XM, MB, SPU, PERM, true>(ctx, p, lds);
+            p.tpw = tpw;
+            p.grid = grid;
+            p.wave_lds = (int)region;
+            // Staging waves (mode 1): one round each, two when the workgroup
+            // owns several tiles (more waves left for K). When they would
+            // take 6 or more waves (long K) or stage the costly silu(a)*b,
+            // each wave stages its own groups instead (mode 2): all waves
+            // stream weights. ST_QMV_STAGE_MODE / _ROUNDS override (tuning).
+            const int mode = env_int("ST_QMV_STAGE_MODE", 0);
+            const int env_r = env_int("ST_QMV_STAGE_ROUNDS", 0);
+            const int r0 = env_r > 0 ? std::min(env_r, kCoopRounds) : (tpw > 1 ? 2 : 1);
+            const long long ns0 = (items + 64 * r0 - 1) / (64 * r0);
+            const bool per_wave = mode == 2 || (mode == 0 && (ns0 >= 6 || XM == XM_SILU));
+            if (!per_wave) {
+                for (int rounds = r0; rounds <= kCoopRounds; ++rounds) {
+                    const long long ns = (items + 64 * rounds - 1) / (64 * rounds);
+                    const long long wpt = (nw - ns) / tpw;  // compute waves per tile in the fullest workgroup
+                    if (wpt < 1) continue;
+                    if (FMT != FMT_I8 && (p.units + wpt - 1) / wpt > kScaleUnits) continue;  // the scale block
+                    p.nstage = (int)ns;
+                    return launch_kernel<FMT, NSRC, XM, MB, SPU, PERM, 1>(ctx, p, lds);
+                }
+                if (mode == 1) return -1;
+            }
+            const int wpt = nw / tpw;
+            if (wpt < 1) return -1;
+            const int upw = (p.units + wpt - 1) / wpt;  // groups per wave
+            if (FMT != FMT_I8 && upw > kScaleUnits) return -1;
+            if ((long long)p.M * upw * IPU > 64ll * kCoopRounds) return -1;  // its staging rounds
+            p.nstage = 0;
+            return launch_kernel<FMT, NSRC, XM, MB, SPU, PERM, 2>(ctx, p, lds);
+        };
+        if (!env_int("ST_QMV_NO_COOP", 0)) {
+            const int ncu = std::max(1, ctx->num_cus);
+            const int tiles_cu = (p.ntiles + ncu - 1) / ncu;
+            if (tiles_cu >= 2 && !env_int("ST_QMV_ONE_TILE", 0)) {
+                // more tiles than CUs: a workgroup per CU (all the waves a CU
+                // holds) owns 2..kMaxTilesPerWg tiles and stages x once for them
+                const int grid = tiles_cu <= kMaxTilesPerWg ? ncu : (p.ntiles + kMaxTilesPerWg - 1) / kMaxTilesPerWg;
+                if ((long long)p.ntiles * grid < (1ll << 31)) {
+                    const int rc = try_coop(NWX, (p.ntiles + grid - 1) / grid, grid);
+                    if (rc != -1) return rc;
+                }
+            }
+            int nw = want >= 16 ? 16 : (want >= 8 ? 8 : 4);
+            nw = std::max(4, std::min({nw, NWX, std::max(4, p.units)}));
+            nw = std::max(4, std::min(NWX, env_int("ST_QMV_WAVES", nw)));
+            // more waves when the staging waves leave too few for K (GPTQ:
+            // at most kScaleUnits groups per wave, the scale block)
+            for (;; nw = std::min(2 * nw, NWX)) {
+                const int rc = try_coop(nw, 1, p.ntiles);
+                if (rc != -1 || nw == NWX) {
+                    if (rc != -1) return rc;
+                    break;
+                }
+            }
         }
     }
-    // fallback: per-wave chunked staging, 4 waves
+    // fallback: per-wave chunked staging, 4 waves, one tile per workgroup
     const int nw = 4;
     p.nwaves = nw;
+    p.tpw = 1;
+    p.grid = p.ntiles;
     const int max_units = (p.units + nw - 1) / nw;
     if (FMT != FMT_I8 && max_units > kMaxZeroUnits && (p.qz[0] || p.qz[1]))
         return fail(ST_ERR_SHAPE, "qmv: %d groups per wave exceed the zero-point table", max_units);
@@ -627,7 +819,7 @@ int launch_t(st_context *ctx, Params &p) {
     const int ztab = (FMT == FMT_I8) ? 0 : std::min(max_units, kMaxZeroUnits) * NSRC * 16;
     p.wave_lds = (afr * 16 + p.chunk * p.M * 12 + ztab + 15) & ~15;
     const size_t lds = (size_t)nw * p.wave_lds + (size_t)nw * NSRC * MB * 64 * sizeof(float);
-    return launch_kernel<FMT, NSRC, XM, MB, SPU, PERM, false>(ctx, p, lds);
+    return launch_kernel<FMT, NSRC, XM, MB, SPU, PERM, 0>(ctx, p, lds);
 }
 
 template <int FMT, int NSRC, int XM, int SPU, bool PERM>

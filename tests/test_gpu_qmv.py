@@ -381,3 +381,41 @@ def test_concatenated_linears_equal_separate_calls(gpu, orc, tiled):
     assert np.array_equal(y, np.concatenate(sep, axis=1))
     with pytest.raises(ValueError):
         sta.GptqWeight.cat([ws[2], ws[0]])  # N = 72 is not a multiple of 16 before the last part
+
+
+@pytest.mark.parametrize("K,N,gs,zeros,act", [
+    (4096, 8200, 128, True, True),      # 513 tiles: 2-3 tiles per workgroup, ragged last tile
+    (2048, 16392, 64, True, False),     # 1025 tiles: 4 tiles per workgroup, grid beyond the CUs
+    (2560, 12296, 256, False, False),   # 769 tiles
+    (1024, 4104, 128, False, True),     # 257 tiles: just past one tile per CU
+])
+def test_multi_tile_workgroups(gpu, orc, K, N, gs, zeros, act, monkeypatch):
+    """N above 16 columns per CU: one workgroup owns several 16-column tiles
+    and stages x once for them. Same values as one tile per workgroup (up to
+    f32 summation order across K slices) and the f64 oracle."""
+    c = orc.gptq_case(K // 64 + N, K, N, gs, zeros=zeros, act_order=act)
+    w = up(gpu, c)
+    y = run_matvec(gpu, w, c["x"])[0]
+    monkeypatch.setenv("ST_QMV_ONE_TILE", "1")
+    y1 = run_matvec(gpu, w, c["x"])[0]
+    ref = orc.gptq_matvec_f64(c["x"], c["qweight"], c["scales"], K, N, gs, qzeros=c["qzeros"], g_idx=c["g_idx"])
+    e, e1 = orc.rel_l2(y, ref), orc.rel_l2(y, y1)
+    print(f"multi-tile K={K} N={N} gs={gs}: rel-L2 {e:.3e}, vs one tile per workgroup {e1:.3e}")
+    assert e < TOL and e1 < 1e-6
+    assert np.all(np.isfinite(y))
+
+
+@pytest.mark.parametrize("N", [11008, 8200])
+def test_gate_up_multi_tile_with_zeros(gpu, orc, N):
+    K, gs = 4096, 128
+    cg = orc.gptq_case(73, K, N, gs, zeros=True)
+    cu = orc.gptq_case(74, K, N, gs, zeros=True)
+    wg_, wu_ = up(gpu, cg), up(gpu, cu)
+    x = torch.from_numpy(cg["x"]).cuda()
+    y = torch.empty(1, N, device="cuda")
+    M.fused_gate_up_silu(gpu, x, wg_.qweight, wg_.scales, wu_.qweight, wu_.scales, y, K, N, gs,
+                         gate_qz=wg_.qzeros, up_qz=wu_.qzeros, flags=wg_.flags)
+    torch.cuda.synchronize()
+    g = orc.gptq_matvec_f64(cg["x"], cg["qweight"], cg["scales"], K, N, gs, qzeros=cg["qzeros"])
+    u = orc.gptq_matvec_f64(cg["x"], cu["qweight"], cu["scales"], K, N, gs, qzeros=cu["qzeros"])
+    assert orc.rel_l2(y.cpu().numpy()[0], orc.silu_gate_f64(g, u)) < TOL
