@@ -9,11 +9,13 @@
 // per-channel path. The math is the reference's: y[n] = sum_k (q - z) * s * x[k]
 // with z = 8 in the reference (gptq_matvec.wgsl:51-58).
 //
-// Design (CDNA4, wave64), one workgroup per 16 output columns:
-//  * A workgroup owns a 16-column tile for the whole of K, so no workgroup
-//    ever talks to another (cross-workgroup release fences and atomics cost
-//    several microseconds per launch on MI355X). Its waves (4..16) split K
-//    by groups and meet once, at the end, in LDS.
+// Design (CDNA4, wave64), 16-column tiles:
+//  * A workgroup owns whole 16-column tiles for the whole of K, so no
+//    workgroup ever talks to another (cross-workgroup release fences and
+//    atomics cost several microseconds per launch on MI355X). Its waves split
+//    K by groups and meet once, at the end, in LDS. When N has more tiles
+//    than the GPU has CUs, one workgroup per CU owns 2..4 tiles (x is staged
+//    once per CU instead of once per tile).
 //  * The dot products run on the int8 matrix cores (v_mfma_i32_16x16x64_i8,
 //    16 rows x 16 columns x 64 k). B = weights: lane (q, c) supplies column c,
 //    k-chunk q. A GPTQ word (8 nibbles of one column) becomes two int8
@@ -27,13 +29,18 @@
 //    including the zero point as -z * sum(X); each group result is rounded to
 //    f32 once and scaled by s * 2^-e. Error ~2^-22 relative, far below the
 //    reference's f32 FMA chain.
-//  * Each wave keeps a ring of D groups of weight loads in flight (registers)
-//    and stages its own slice of x into a private LDS buffer, with
-//    cross-lane shuffles for the per-group max and sum: no barrier until the
-//    final reduction.
+//  * Each wave keeps a ring of D groups of weight loads in flight (registers).
+//  * Staging x (the decode case, one token block): either a few staging
+//    waves that load no weights stage all of K into shared LDS, one or two
+//    64-item rounds each, while the other waves start streaming weights and
+//    wait at one bare barrier that leaves their loads in flight; or, for long
+//    K, every wave stages its own groups (no barrier). Group max and sum use
+//    DPP row moves; the integer conversion is one FMA. Several tokens and
+//    long K: each wave stages its own chunks (fallback).
 //  * vmcnt discipline: global loads complete in issue order and the compiler
 //    counts them per path. Every load the wave issues while the ring is in
-//    flight is unconditional (absent items read a clamped valid address) and
+//    flight is unconditional (absent items read a clamped valid address, or,
+//    with buffer loads, an out-of-range offset that accesses nothing) and
 //    act-order is a template parameter, so no uniform branch changes the
 //    number of loads in flight; otherwise the compiler's waits can be too
 //    loose across the merge and registers are read before their loads land.
@@ -225,8 +232,8 @@ constexpr int kScaleUnits = 16;  // groups per wave covered by the COOP scale bl
 template <int FMT, int NSRC, int SPU, bool COOP>
 constexpr int ring_depth() {
     constexpr int WPU = (FMT == FMT_I8) ? 4 * SPU : 2 * SPU;
-    // (COOP keeps the depth it had with the scale in the ring: deeper rings
-    // measured slower, more registers and more loads queued at issue)
+    // (COOP keeps the depth it had with the scale in the ring: rings of 6
+    // and 8 measured slower, more registers and more loads queued at issue)
     constexpr int RPU = NSRC * (WPU + (FMT == FMT_I8 ? 0 : 1));
     constexpr int budget = (COOP && NSRC == 2) ? 40 : 24;
     return (budget / RPU) < 2 ? 2 : ((budget / RPU) > 6 ? 6 : (budget / RPU));
