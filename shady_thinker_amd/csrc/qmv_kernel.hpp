@@ -224,6 +224,10 @@ constexpr int kMaxTilesPerWg = 4;  // COOP: tiles one workgroup may own
 constexpr int kRingBeforeBarrier = 2;
 
 constexpr int kCoopRounds = 4;  // x staging rounds per staging wave in COOP kernels
+// CHK kernels: consecutive groups per wave per K chunk (the ring depth); 3
+// and 4 measured slower (32 INT8 tokens: 84 and 119 against 65 us)
+constexpr int kChunkSlots = 2;
+constexpr int kChunkRounds = 2;  // CHK kernels: x staging rounds per wave per chunk
 constexpr int kScaleUnits = 16;  // groups per wave covered by the COOP scale block (two loads per source)
 
 // Prefetch ring depth: the registers of weights in flight per lane, about 24
@@ -240,19 +244,22 @@ constexpr int ring_depth() {
 }
 
 // CM (staging mode): 0 = per-wave chunks (fallback), 1 = cooperative with
-// staging waves, 2 = cooperative, each wave staging its own groups.
+// staging waves, 2 = cooperative, each wave staging its own groups, 3 =
+// cooperative in K chunks (several token blocks: all waves stage each chunk,
+// each wave computes kChunkSlots consecutive groups of every chunk).
 template <int FMT, int NSRC, int XM, int MB, int SPU, bool PERM, int CM>
 __global__ __launch_bounds__((64 * kMaxWavesFor<NSRC, (CM != 0)>)) void qmv_kernel(Params p) {
     constexpr bool COOP = CM != 0;
+    constexpr bool CHK = CM == 3;
     extern __shared__ __align__(16) unsigned char smem[];
-    constexpr int D = ring_depth<FMT, NSRC, SPU, COOP>();
+    constexpr int D = CHK ? kChunkSlots : ring_depth<FMT, NSRC, SPU, COOP>();
     constexpr int DPRE = kRingBeforeBarrier < D ? kRingBeforeBarrier : D;  // COOP: slots before the barrier
     constexpr int IPU = 4 * SPU;                              // 16-k items per group and token
     constexpr int WPU = (FMT == FMT_I8) ? 4 * SPU : 2 * SPU;  // weight dwords per lane per group
     // staging rounds per lane: per-wave chunk (fallback) or whole slice (COOP)
-    constexpr int RMAX = COOP ? kCoopRounds : (4 * MB * IPU + 63) / 64;
+    constexpr int RMAX = CHK ? kChunkRounds : (COOP ? kCoopRounds : (4 * MB * IPU + 63) / 64);
 
-    constexpr bool SCB = COOP && FMT != FMT_I8;  // per-wave scale block (see below)
+    constexpr bool SCB = (CM == 1 || CM == 2) && FMT != FMT_I8;  // per-wave scale block (see below)
     const int tid = threadIdx.x;
     const int lane = tid & 63;
     const int wave = tid >> 6;
@@ -278,20 +285,23 @@ __global__ __launch_bounds__((64 * kMaxWavesFor<NSRC, (CM != 0)>)) void qmv_kern
     // each); the others split the tiles' K. Fallback: every wave stages its
     // own chunk.
     constexpr bool PW = CM == 2;  // per-wave staging of the wave's own groups, no staging waves
-    const int CH = COOP ? p.units : p.chunk;  // units the A region holds
-    const int NS = (COOP && !PW) ? p.nstage : 0;  // host: ceil(items / 64 RMAX) <= NS <= NW - TB
+    const int CH = (COOP && !CHK) ? p.units : p.chunk;  // units the A region holds
+    const int NS = (CM == 1) ? p.nstage : 0;  // host: ceil(items / 64 RMAX) <= NS <= NW - TB
     const int cw = wave - NS;             // compute-wave index (< 0: a staging wave)
-    const int WPT = (NW - NS) / TB;       // compute waves per tile; the rest idle
+    // compute waves per tile; the rest idle (CHK: fixed by the chunk, CH =
+    // WPT * D, for every workgroup; waves beyond TB * WPT only stage)
+    const int WPT = CHK ? p.chunk / D : (NW - NS) / TB;
     const int tj = cw >= 0 ? cw % TB : 0;  // tile slot of this wave
     const int ks = cw >= 0 ? cw / TB : WPT;  // K slice of this wave (WPT: none)
     const int tile = t0 + tj;
     const int n0 = tile * kTileN;
     const int ncol = min(n0 + c, N - 1);  // clamped column this lane loads
 
-    const int u0 = ks < WPT ? (int)((unsigned)(ks * p.units) / (unsigned)WPT) : 0;
-    const int u1 = ks < WPT ? (int)((unsigned)((ks + 1) * p.units) / (unsigned)WPT) : 0;
-    const int SW = PW ? u1 - u0 : CH;  // units staged by this wave's staging rounds
-    const int items = M * SW * IPU;
+    // contiguous K slice [u0, u1) (CHK: none; see its loop)
+    const int u0 = (ks < WPT && !CHK) ? (int)((unsigned)(ks * p.units) / (unsigned)WPT) : 0;
+    const int u1 = (ks < WPT && !CHK) ? (int)((unsigned)((ks + 1) * p.units) / (unsigned)WPT) : 0;
+    int SW = PW ? u1 - u0 : CH;  // units staged by the staging rounds (CHK: per chunk)
+    int items = M * SW * IPU;
 
     // LDS: A operands [unit][step][mb][q][row] (16 B each), per (unit, token)
     // 2^-e, -H, -L (sum(X) = H*65536 + L), zero points [unit][src][column].
@@ -381,7 +391,7 @@ __global__ __launch_bounds__((64 * kMaxWavesFor<NSRC, (CM != 0)>)) void qmv_kern
                     U.w[src][4 * st + 3] = t.w;
                 }
             }
-            if constexpr (FMT != FMT_I8 && !COOP) U.s[src] = p.sc[src][(size_t)u * N + ncol];
+            if constexpr (FMT != FMT_I8 && !SCB) U.s[src] = p.sc[src][(size_t)u * N + ncol];
         }
     };
 
@@ -396,9 +406,9 @@ __global__ __launch_bounds__((64 * kMaxWavesFor<NSRC, (CM != 0)>)) void qmv_kern
     // a clamped valid address).
     const int span = COOP ? 64 * NW : 64;
     const int tt = COOP ? tid : lane;
-    const int rstep = (COOP && !PW) ? NS : 1;  // row stride between rounds
+    const int rstep = CHK ? NW : ((COOP && !PW) ? NS : 1);  // row stride between rounds
     const int wave0 = (COOP && !PW) ? wave : 0;  // row of round 0
-    const int uend = (COOP && !PW) ? p.units : u1;  // staged groups end here
+    int uend = (COOP && !PW) ? p.units : u1;  // staged groups end here (CHK: per chunk)
     float xv[RMAX][16];
     // A wave with no item in a round skips it (loads and work): the branch
     // is uniform per wave and the same condition guards the loads and their
@@ -430,7 +440,7 @@ __global__ __launch_bounds__((64 * kMaxWavesFor<NSRC, (CM != 0)>)) void qmv_kern
                 w = i - m * (SW * IPU);
             }
             const int ui = w / IPU, ii = w % IPU;
-            const int ua = COOP ? cs + ui : ui;  // A-region unit (COOP: the group itself)
+            const int ua = (COOP && !CHK) ? cs + ui : ui;  // A-region unit (COOP: the group itself)
             const bool ok = i < items && cs + ui < uend;
             float amax = 0.0f, nf = 0.0f;
 #pragma unroll
@@ -513,6 +523,12 @@ __global__ __launch_bounds__((64 * kMaxWavesFor<NSRC, (CM != 0)>)) void qmv_kern
     // writes both, in order).
     if constexpr (!COOP)
         for (int i = tt; i < afrags; i += span) abuf[i] = u32x4{0, 0, 0, 0};
+    // CHK: rows of absent tokens (M not a multiple of 4) are zeroed once; no
+    // staging item ever writes them, so this races with nothing.
+    if constexpr (CHK)
+        if (M < 4 * MB)
+            for (int i = tid; i < afrags; i += 64 * NW)
+                if ((i / (RB * 4)) % MB * 4 + (i % RB) / 4 >= M) abuf[i] = u32x4{0, 0, 0, 0};
 
     // --------------------------------------------------------- main loop
     float tot[NSRC][MB];
@@ -565,7 +581,7 @@ __global__ __launch_bounds__((64 * kMaxWavesFor<NSRC, (CM != 0)>)) void qmv_kern
                 if constexpr (FMT == FMT_I8) {
                     f = em;
                 } else {
-                    const uint16_t sh = COOP ? s_sc[(wave * NSRC + src) * 256 + (u - u0) * 16 + c] : U.s[src];
+                    const uint16_t sh = SCB ? s_sc[(wave * NSRC + src) * 256 + (u - u0) * 16 + c] : U.s[src];
                     f = (float)__builtin_bit_cast(_Float16, sh) * em;
                     z = have_z[src] ? (int)s_z[((tj * ZU + u - zbase) * NSRC + src) * 16 + c] : 8;
                 }
@@ -586,6 +602,48 @@ __global__ __launch_bounds__((64 * kMaxWavesFor<NSRC, (CM != 0)>)) void qmv_kern
         stage(u);
     };
 
+    if constexpr (CHK) {
+        // K in chunks of CH = WPT * D groups; in chunk cc, compute wave
+        // (tile tj, slice ks) owns groups cc*CH + ks*D + d, d < D, which are
+        // its ring slots. Per chunk: x of the next chunk is loaded (into
+        // registers) before this chunk's groups are computed and the ring
+        // is refilled with the next chunk's groups; then all waves stage the
+        // next chunk between two bare barriers (the ring stays in flight).
+        // Every load is unconditional (the last chunk's x is loaded again
+        // at the end; groups past K are empty slots).
+        const int nch = (p.units + CH - 1) / CH;
+        int cs = 0;
+        auto set_chunk = [&](int cc) {
+            cs = cc * CH;
+            uend = min(cs + CH, p.units);
+            SW = uend - cs;
+            items = M * SW * IPU;
+        };
+        const bool comp = ks < WPT;  // a compute wave (others only stage)
+        set_chunk(0);
+        xload(cs);
+#pragma unroll
+        for (int d = 0; d < D; ++d) {
+            const int u = ks * D + d;
+            load_unit(ring[d], min(u, p.units - 1), comp && u < p.units);
+        }
+        stage(cs);
+        asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+        for (int cc = 0; cc < nch; ++cc) {
+            set_chunk(min(cc + 1, nch - 1));
+            xload(cs);
+#pragma unroll
+            for (int d = 0; d < D; ++d) {
+                const int u = cc * CH + ks * D + d;
+                if (comp && u < p.units) compute(ring[d], u, u - cc * CH);
+                const int un = u + CH;
+                load_unit(ring[d], min(un, p.units - 1), comp && cc + 1 < nch && un < p.units);
+            }
+            asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");  // chunk cc's A operands are free
+            if (cc + 1 < nch) stage(cs);
+            asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");  // chunk cc + 1 is staged
+        }
+    } else {
     // COOP: the staging waves load x, wait for it and stage it; they issue no
     // weight load, so neither x nor the staging queues behind the weight
     // stream at the CU's memory port, and the other waves start streaming at
@@ -681,6 +739,8 @@ __global__ __launch_bounds__((64 * kMaxWavesFor<NSRC, (CM != 0)>)) void qmv_kern
         }
     }
 
+    }
+
     // ------------------------------------------- reduce the waves, write y
     float *red = reinterpret_cast<float *>(smem + (COOP ? (size_t)p.wave_lds : (size_t)NW * p.wave_lds));
 #pragma unroll
@@ -733,6 +793,7 @@ int launch_kernel(st_context *ctx, Params &p, size_t lds) {
 }
 
 constexpr size_t kCoopLdsBudget = 96 * 1024;
+constexpr size_t kChunkLdsBudget = 150 * 1024;  // one workgroup per CU
 
 template <int FMT, int NSRC, int XM, int MB, int SPU, bool PERM>
 int launch_t(st_context *ctx, Params &p) {
@@ -811,6 +872,35 @@ int launch_t(st_context *ctx, Params &p) {
                     if (rc != -1) return rc;
                     break;
                 }
+            }
+        }
+    }
+    // Several token blocks, more tiles than CUs: K-chunked cooperative
+    // staging (CM 3), a workgroup per CU owning 2..kMaxTilesPerWg tiles.
+    // (up to 16 tokens: calls with more run as 16-token blocks, and 8 token
+    // blocks would not fit the registers)
+    if constexpr (MB > 1 && MB <= 4 && FMT != FMT_I4) {
+        constexpr int NWX = kMaxWavesFor<NSRC, true>;
+        const int ncu = std::max(1, ctx->num_cus);
+        const int tiles_cu = (p.ntiles + ncu - 1) / ncu;
+        if (tiles_cu >= 2 && !env_int("ST_QMV_NO_CHUNK", 0)) {
+            const int grid = tiles_cu <= kMaxTilesPerWg ? ncu : (p.ntiles + kMaxTilesPerWg - 1) / kMaxTilesPerWg;
+            const int tpw = (p.ntiles + grid - 1) / grid;
+            const int nw = NWX, wpt = nw / tpw;
+            const int ch = wpt * kChunkSlots;
+            const size_t a_bytes = (size_t)ch * ((size_t)SPU * MB * 4 * p.rb * 16 + (size_t)p.M * 12);
+            const size_t region =
+                (a_bytes + (FMT != FMT_I8 ? (size_t)tpw * p.units * NSRC * 16 : 0) + 15) & ~size_t(15);
+            const size_t lds = region + (size_t)nw * NSRC * MB * 64 * sizeof(float);
+            if ((long long)p.ntiles * grid < (1ll << 31) && wpt >= 1 &&
+                (long long)p.M * ch * IPU <= 64ll * kChunkRounds * nw && lds <= kChunkLdsBudget) {
+                p.nwaves = nw;
+                p.tpw = tpw;
+                p.grid = grid;
+                p.chunk = ch;
+                p.nstage = 0;
+                p.wave_lds = (int)region;
+                return launch_kernel<FMT, NSRC, XM, MB, SPU, PERM, 3>(ctx, p, lds);
             }
         }
     }

@@ -419,3 +419,45 @@ def test_gate_up_multi_tile_with_zeros(gpu, orc, N):
     g = orc.gptq_matvec_f64(cg["x"], cg["qweight"], cg["scales"], K, N, gs, qzeros=cg["qzeros"])
     u = orc.gptq_matvec_f64(cg["x"], cu["qweight"], cu["scales"], K, N, gs, qzeros=cu["qzeros"])
     assert orc.rel_l2(y.cpu().numpy()[0], orc.silu_gate_f64(g, u)) < TOL
+
+
+@pytest.mark.parametrize("K,N,gs,Mr,zeros,act", [
+    (2048, 8200, 128, 6, True, True),     # 513 tiles, 3 per workgroup: chunks of 10 groups (10 + 6)
+    (4096, 4104, 64, 13, False, False),   # 257 tiles, 2 per workgroup
+    (2560, 16392, 256, 16, True, False),  # 1025 tiles, 4 per workgroup: chunks of 8 groups (8 + 2)
+    (5120, 13824, 128, 8, False, True),   # configs[2]-sized GPTQ, two token blocks
+])
+def test_multi_token_chunked(gpu, orc, K, N, gs, Mr, zeros, act, monkeypatch):
+    """Several token blocks on a multi-tile grid: x staged cooperatively in K
+    chunks once per CU. Same values as the per-wave fallback (up to f32
+    summation order) and the f64 oracle, every token row."""
+    c = orc.gptq_case(K // 32 + N + Mr, K, N, gs, zeros=zeros, act_order=act, M=Mr)
+    w = up(gpu, c)
+    y = run_matvec(gpu, w, c["x"])
+    monkeypatch.setenv("ST_QMV_NO_CHUNK", "1")
+    y0 = run_matvec(gpu, w, c["x"])
+    ref = orc.gptq_matvec_f64(c["x"], c["qweight"], c["scales"], K, N, gs, qzeros=c["qzeros"], g_idx=c["g_idx"])
+    e, e0 = orc.rel_l2(y, ref), orc.rel_l2(y, y0)
+    print(f"chunked K={K} N={N} gs={gs} M={Mr}: rel-L2 {e:.3e}, vs fallback {e0:.3e}")
+    assert e < TOL and e0 < 1e-6
+    for m in range(Mr):
+        assert orc.rel_l2(y[m], ref[m]) < TOL
+
+
+def test_gate_up_multi_token_chunked_with_zeros(gpu, orc):
+    K, N, gs, Mr = 4096, 11008, 128, 7
+    cg = orc.gptq_case(75, K, N, gs, zeros=True, M=Mr)
+    cu = orc.gptq_case(76, K, N, gs, zeros=True)
+    wg_, wu_ = up(gpu, cg), up(gpu, cu)
+    x = torch.from_numpy(cg["x"]).cuda()
+    y = torch.empty(Mr, N, device="cuda")
+    M.fused_gate_up_silu(gpu, x, wg_.qweight, wg_.scales, wu_.qweight, wu_.scales, y, K, N, gs,
+                         gate_qz=wg_.qzeros, up_qz=wu_.qzeros, flags=wg_.flags)
+    torch.cuda.synchronize()
+    g = orc.gptq_matvec_f64(cg["x"], cg["qweight"], cg["scales"], K, N, gs, qzeros=cg["qzeros"])
+    u = orc.gptq_matvec_f64(cg["x"], cu["qweight"], cu["scales"], K, N, gs, qzeros=cu["qzeros"])
+    ref = orc.silu_gate_f64(g, u)
+    y = y.cpu().numpy()
+    assert orc.rel_l2(y, ref) < TOL
+    for m in range(Mr):
+        assert orc.rel_l2(y[m], ref[m]) < TOL
