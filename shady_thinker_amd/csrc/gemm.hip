@@ -1,20 +1,17 @@
 // Prefill GEMM on gfx950: C[M, N] = A[M, K] (f16) . dequant(W), W GPTQ int4.
 // No reference counterpart: the reference prefills token by token through
 // the matvec (src/inference.rs:93-95). Dequant semantics are the reference's
-// ((q - z) * s, src/shaders/gptq_matvec.wgsl:51-58) and stay exact:
+// ((q - z) * s, src/shaders/gptq_matvec.wgsl:51-58):
 //
-//  * B operand = (q - z) as integer-valued f16 (exact: |q - z| <= 15). A
-//    GPTQ word holds 8 consecutive k of one column, which is exactly one
-//    lane's B fragment of v_mfma_f32_32x32x16_f16, so weights go straight
-//    from HBM to registers (no LDS). Word -> 4 f16 pairs in 9 VALU ops:
-//    and-or of the even nibble pairs into the f16 1024 bias (1024 + q),
-//    of the odd pairs in place (1024 + 16 q), one shift by 8 for the upper
-//    half; then one packed subtract (- (1024 + z)) or one packed fma
-//    (* 1/16 - (64 + z)) per pair. Every step is exact in f16.
-//  * Each group (128 k) accumulates in f32 from zero; its partial is then
-//    multiplied by the column's f16 scale and added to the running total.
-//    So the only roundings are the MFMA's f32 accumulation and one f32
-//    multiply-add per group, as in an f32 dequant-then-GEMM.
+//  * B operand = (q - z) * s rounded once to f16 per weight (the dequant of
+//    the usual f16 GPTQ GEMMs; rel-L2 ~2e-4 against the f64 oracle, bar
+//    2e-3). A GPTQ word holds 8 consecutive k of one column, which is exactly
+//    one lane's B fragment of v_mfma_f32_32x32x16_f16, so weights go straight
+//    from HBM to registers (no LDS). Word -> 4 f16 pairs: and-or of the even
+//    nibble pairs into the f16 1024 bias (1024 + q) and of the odd pairs in
+//    place (1024 + 16 q), one shift by 8 for the upper half, then one packed
+//    subtract (- (1024 + z)) or packed fma (* 1/16 - (64 + z)) per pair,
+//    which forms (q - z) exactly, and one packed multiply by the scale.
 //  * A (activations, f16) first goes through a pre-pass (prep_a_kernel)
 //    into the context workspace: act-order column gather if any, and each
 //    8-k chunk reordered to the B register order (k = 0,4,1,5,2,6,3,7), so A
@@ -26,11 +23,12 @@
 //  * Workgroup tile 128 (M) x 256 (N), 4 waves side by side along N, each
 //    wave 128 x 64 = 4 x 2 MFMA blocks of 32 x 32: every converted B
 //    fragment feeds 4 MFMAs, every A fragment read from LDS feeds 2, and no
-//    B column is converted twice in a workgroup. Group partials + totals take
-//    256 registers: one wave per SIMD, latency hidden by the one-tile-ahead
-//    prefetch of A (registers -> LDS) and B (registers). Tiles are ordered
-//    XCD-major: the workgroups of one XCD share A rows, which then stay in
-//    that XCD's L2.
+//    B column is converted twice in a workgroup. 128 accumulator registers,
+//    two waves per SIMD; B words and the next k-step's A fragments are read
+//    one step ahead. Tiles are ordered XCD-major: the workgroups of one XCD
+//    share A rows, which then stay in that XCD's L2.
+//  * Small grids split K (f32 partials in the workspace, a fixed-order
+//    reduce kernel).
 //  * Act-order: K is sorted by group at upload (st_gptq_i4_act_order); the
 //    matching column gather of A is part of the pre-pass.
 #include "common.hpp"
@@ -94,11 +92,15 @@ __device__ __forceinline__ half8 word_to_b(unsigned w, const BConv &c) {
     return __builtin_bit_cast(half8, r);
 }
 
-template <int GS, bool TILED, bool F16OUT>
+// CB_ = 32-column MFMA blocks per wave: 2 (workgroup tile 128 x 256) or 1
+// (128 x 128, for grids whose 128 x 256 tiles would leave CUs idle).
+template <int GS, bool TILED, bool F16OUT, int CB_>
 __global__ __launch_bounds__(kThreads, kWavesPerSimd) void gemm_kernel(const _Float16 *__restrict__ A, const uint32_t *__restrict__ qw,
                                                            const uint16_t *__restrict__ sc, const uint32_t *__restrict__ qz,
                                                            int zoff, void *__restrict__ C, int M, int K, int N,
                                                            int kps, float *__restrict__ part) {
+    constexpr int CB = CB_;            // (hides the namespace-scope defaults)
+    constexpr int BN = 32 * CB * WN;
     // Two separate arrays (not one [2][...]) so that alias analysis can tell
     // the stage being read from the stage the DMA is filling; otherwise every
     // LDS read waits for the in-flight DMA.
@@ -403,18 +405,26 @@ struct Split {
     float *part;  // nullptr when S == 1
 };
 
-template <int GS, bool TILED>
-int launch_gs(st_context *ctx, const _Float16 *A, const uint32_t *qw, const uint16_t *sc, const uint32_t *qz, int zoff,
+template <int GS, bool TILED, int CBL>
+int launch_cb(st_context *ctx, const _Float16 *A, const uint32_t *qw, const uint16_t *sc, const uint32_t *qz, int zoff,
               void *C, bool f16out, int M, int K, int N, const Split &sp) {
-    const int T = ((M + BM - 1) / BM) * ((N + BN - 1) / BN);
+    const int T = ((M + BM - 1) / BM) * ((N + 32 * CBL * WN - 1) / (32 * CBL * WN));
     const dim3 grid(T * sp.S);
     if (f16out)
-        hipLaunchKernelGGL((gemm_kernel<GS, TILED, true>), grid, dim3(kThreads), 0, ctx->stream, A, qw, sc, qz, zoff, C, M,
-                           K, N, sp.kps, sp.part);
+        hipLaunchKernelGGL((gemm_kernel<GS, TILED, true, CBL>), grid, dim3(kThreads), 0, ctx->stream, A, qw, sc, qz, zoff,
+                           C, M, K, N, sp.kps, sp.part);
     else
-        hipLaunchKernelGGL((gemm_kernel<GS, TILED, false>), grid, dim3(kThreads), 0, ctx->stream, A, qw, sc, qz, zoff, C,
-                           M, K, N, sp.kps, sp.part);
-    if (int rc = st::launch_check("gemm_kernel")) return rc;
+        hipLaunchKernelGGL((gemm_kernel<GS, TILED, false, CBL>), grid, dim3(kThreads), 0, ctx->stream, A, qw, sc, qz, zoff,
+                           C, M, K, N, sp.kps, sp.part);
+    return st::launch_check("gemm_kernel");
+}
+
+template <int GS, bool TILED>
+int launch_gs(st_context *ctx, const _Float16 *A, const uint32_t *qw, const uint16_t *sc, const uint32_t *qz, int zoff,
+              void *C, bool f16out, int M, int K, int N, int cb, const Split &sp) {
+    const int rc = cb == 1 ? launch_cb<GS, TILED, 1>(ctx, A, qw, sc, qz, zoff, C, f16out, M, K, N, sp)
+                           : launch_cb<GS, TILED, 2>(ctx, A, qw, sc, qz, zoff, C, f16out, M, K, N, sp);
+    if (rc) return rc;
     if (sp.S > 1) {
         const size_t MN = (size_t)M * N;
         const dim3 rg((unsigned)((MN / 4 + 255) / 256));
@@ -429,12 +439,22 @@ int launch_gs(st_context *ctx, const _Float16 *A, const uint32_t *qw, const uint
 
 template <bool TILED>
 int launch_tiled(st_context *ctx, const _Float16 *A, const uint32_t *qw, const uint16_t *sc, const uint32_t *qz, int zoff,
-                 void *C, bool f16out, int M, int K, int N, int gs, const Split &sp) {
+                 void *C, bool f16out, int M, int K, int N, int gs, int cb, const Split &sp) {
     switch (gs) {
-        case 64: return launch_gs<64, TILED>(ctx, A, qw, sc, qz, zoff, C, f16out, M, K, N, sp);
-        case 128: return launch_gs<128, TILED>(ctx, A, qw, sc, qz, zoff, C, f16out, M, K, N, sp);
-        default: return launch_gs<256, TILED>(ctx, A, qw, sc, qz, zoff, C, f16out, M, K, N, sp);
+        case 64: return launch_gs<64, TILED>(ctx, A, qw, sc, qz, zoff, C, f16out, M, K, N, cb, sp);
+        case 128: return launch_gs<128, TILED>(ctx, A, qw, sc, qz, zoff, C, f16out, M, K, N, cb, sp);
+        default: return launch_gs<256, TILED>(ctx, A, qw, sc, qz, zoff, C, f16out, M, K, N, cb, sp);
     }
+}
+
+// 32-column blocks per wave: 1 (128 x 128 tiles) when 128 x 256 tiles would
+// give at most one workgroup per CU (then two waves per SIMD instead of
+// one); ST_GEMM_CB forces 1 or 2.
+int pick_cb(st_context *ctx, int M, int N) {
+    const char *e = std::getenv("ST_GEMM_CB");
+    if (e && (*e == '1' || *e == '2')) return *e - '0';
+    const int T2 = ((M + BM - 1) / BM) * ((N + BN - 1) / BN);
+    return T2 <= ctx->num_cus ? 1 : 2;
 }
 
 // Split K when the tiles alone fill at most half the CUs (the f32 partials
@@ -442,9 +462,9 @@ int launch_tiled(st_context *ctx, const _Float16 *A, const uint32_t *qw, const u
 // configs[3] M = 512, 224 tiles): S splits of an even number of K tiles
 // each, as many as fill the workgroup slots (two per CU), at most 8, each at
 // least 4 K tiles, within the workspace left after A'.
-Split plan_split(st_context *ctx, int M, int K, int N, size_t ws_used) {
+Split plan_split(st_context *ctx, int M, int K, int N, int cb, size_t ws_used) {
     Split sp{1, K / KT, nullptr};
-    const int T = ((M + BM - 1) / BM) * ((N + BN - 1) / BN);
+    const int T = ((M + BM - 1) / BM) * ((N + 32 * cb * WN - 1) / (32 * cb * WN));
     const int slots = 2 * ctx->num_cus;
     const int ntiles = K / KT;
     const char *no_split = std::getenv("ST_GEMM_NO_SPLIT");
@@ -490,8 +510,9 @@ extern "C" int st_gptq_i4_gemm(st_context *ctx, const uint16_t *a, const uint32_
     if (int rc = st::launch_check("prep_a_kernel")) return rc;
     const int zoff = (flags & ST_FLAG_ZEROS_PLUS_ONE) ? 1 : 0;
     const bool f16out = c_dtype == ST_F16;
-    const Split sp = plan_split(ctx, M, K, N, need);
+    const int cb = pick_cb(ctx, M, N);
+    const Split sp = plan_split(ctx, M, K, N, cb, need);
     if (flags & ST_FLAG_TILED)
-        return launch_tiled<true>(ctx, A, qweight, scales, qzeros, zoff, c, f16out, M, K, N, group_size, sp);
-    return launch_tiled<false>(ctx, A, qweight, scales, qzeros, zoff, c, f16out, M, K, N, group_size, sp);
+        return launch_tiled<true>(ctx, A, qweight, scales, qzeros, zoff, c, f16out, M, K, N, group_size, cb, sp);
+    return launch_tiled<false>(ctx, A, qweight, scales, qzeros, zoff, c, f16out, M, K, N, group_size, cb, sp);
 }
