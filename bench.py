@@ -456,13 +456,22 @@ def bench_int8(torch, dev, gpu, Mdl, gen, args):
     activations, M = 1 / 8 / 32 (matvec to skinny GEMM), 4 cold copies."""
     K, N, copies = 5120, 13824, 4
     ws = [torch.randint(-127, 128, (N, K), device=dev, dtype=torch.int8, generator=gen) for _ in range(copies)]
+    from shady_thinker_amd._lib import ST_FLAG_TILED, call, lib
+
+    def tile8(w):  # the upload-time layout (Int8Weight.upload)
+        t = torch.empty(lib().st_int8_tiled_bytes(K, N), dtype=torch.int8, device=dev)
+        gpu.sync_stream()
+        call("st_int8_repack", gpu.handle, w.data_ptr(), t.data_ptr(), K, N)
+        return t
+
+    ws = [tile8(w) for w in ws]
     sc = (torch.randn(N, device=dev, generator=gen) * 0.01).abs()
     out = {"K": K, "N": N}
     for Mr in (1, 8, 32):
         x = torch.randn(Mr, K, device=dev, generator=gen).half()
         y = torch.empty(Mr, N, device=dev)
         iters = max(20, min(100, args.steps // 2))
-        ms = Replayer(torch, lambda i: Mdl.int8_matvec(gpu, x, ws[i % copies], sc, y, K, N), copies).run(iters, 4)
+        ms = Replayer(torch, lambda i: Mdl.int8_matvec(gpu, x, ws[i % copies], sc, y, K, N, ST_FLAG_TILED), copies).run(iters, 4)
         b = K * N + 4 * N + 2 * Mr * K + 4 * Mr * N
         out[f"M{Mr}"] = {"ms": round(ms, 5), "GB/s": round(b / (ms * 1e-3) / 1e9, 1),
                          "hbm_frac": round(b / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),

@@ -56,7 +56,7 @@ typedef enum { ST_F32 = 0, ST_F16 = 1, ST_BF16 = 2 } st_dtype;
 
 /* flags */
 #define ST_FLAG_ZEROS_PLUS_ONE 0x1u /* qzeros hold z - 1 (AutoGPTQ v1 files) */
-#define ST_FLAG_TILED 0x2u          /* qweight is in the tiled layout of st_gptq_i4_repack */
+#define ST_FLAG_TILED 0x2u          /* weights in the tiled layout of st_gptq_i4_repack / st_int8_repack */
 
 /* ------------------------------------------------------------ runtime */
 
@@ -197,9 +197,18 @@ int st_gptq_i4_gemm(st_context *ctx, const uint16_t *a, const uint32_t *qweight,
 
 /* y[M, N] = x[M, K] . (w[N, K]^T * scale[N]), int8 symmetric per output
  * channel. No reference counterpart. x in x_dtype (ST_F16 or ST_F32),
- * 1 <= M <= 32, K % 128 == 0, N % 4 == 0. */
+ * 1 <= M <= 32, K % 128 == 0, N % 4 == 0. flags: ST_FLAG_TILED when w is in
+ * the layout of st_int8_repack (else row-major int8[N, K]). */
 int st_int8_matvec(st_context *ctx, const void *x, int x_dtype, const int8_t *w,
-                   const float *scale, float *y, int M, int K, int N);
+                   const float *scale, float *y, int M, int K, int N, uint32_t flags);
+
+/* Upload-time INT8 repack (no reference counterpart): row-major w[N, K] ->
+ * tiles of 16 rows in which, per 128-k group, each of a wave's 64 lanes
+ * holds 32 contiguous bytes, so the kernel reads 2 KiB contiguous per group.
+ * Values are unchanged (a permutation of 16-byte pieces). w_tiled must hold
+ * st_int8_tiled_bytes(K, N) bytes; pass ST_FLAG_TILED to st_int8_matvec. */
+size_t st_int8_tiled_bytes(int K, int N);
+int st_int8_repack(st_context *ctx, const int8_t *w, int8_t *w_tiled, int K, int N);
 
 #ifdef __cplusplus
 }

@@ -17,7 +17,7 @@ CSRC = os.path.join(HERE, "csrc")
 OBJ = os.path.join(HERE, "_build")
 LIB = os.path.join(HERE, "libshady_hip.so")
 SOURCES = [
-    "runtime.hip", "qmv.hip", "qmv_i4_p0.hip", "qmv_i4_p1.hip", "qmv_i4t_p0.hip", "qmv_i4t_p1.hip", "qmv_i8.hip",
+    "runtime.hip", "qmv.hip", "qmv_i4_p0.hip", "qmv_i4_p1.hip", "qmv_i4t_p0.hip", "qmv_i4t_p1.hip", "qmv_i8.hip", "qmv_i8t.hip",
     "dequant.hip", "gemm.hip", "bf16mv.hip",
 ]
 

@@ -16,6 +16,8 @@ template <>
 int dispatch<FMT_I4T, true>(st_context *, Params &, int, int);
 template <>
 int dispatch<FMT_I8, false>(st_context *, Params &, int, int);
+template <>
+int dispatch<FMT_I8T, false>(st_context *, Params &, int, int);
 }  // namespace qmv
 }  // namespace st
 
@@ -43,6 +45,25 @@ __global__ __launch_bounds__(256) void repack_kernel(const uint32_t *__restrict_
     const int n = min(16 * T + c, N - 1);
     const size_t pr = (size_t)g * (gs / 8) + st * 8 + 2 * q + h;
     out[idx] = qw[pr * N + n];
+}
+
+// Re-tile INT8 w [N, K]: tile T (16 rows), group u (128 k), lane (q, c)
+// gets 32 contiguous bytes, k = 128 u + 16 q + 64 st + j (st < 2, j < 16) of
+// row 16 T + c (rows past N repeat row N - 1). One thread per 16 bytes.
+__global__ __launch_bounds__(256) void repack8_kernel(const int8_t *__restrict__ w, int8_t *__restrict__ out, int K,
+                                                      int N, int ntiles) {
+    const int units = K / 128;
+    const long long total = (long long)ntiles * units * 64 * 2;
+    const long long idx = (long long)blockIdx.x * blockDim.x + threadIdx.x;
+    if (idx >= total) return;
+    const int st = (int)(idx & 1);
+    const int lane = (int)((idx >> 1) & 63);
+    const long long tu = idx >> 7;
+    const int u = (int)(tu % units);
+    const int T = (int)(tu / units);
+    const int n = min(16 * T + (lane & 15), N - 1);
+    const size_t k0 = (size_t)u * 128 + 16 * (lane >> 4) + 64 * st;
+    reinterpret_cast<uint4 *>(out)[idx] = *reinterpret_cast<const uint4 *>(w + (size_t)n * K + k0);
 }
 
 int launch_i4(st_context *ctx, QmvParams &p, bool tiled, int nsrc, int xm) {
@@ -196,13 +217,31 @@ int st_gptq_i4_repack(st_context *ctx, const uint32_t *qweight, uint32_t *qweigh
     return st::launch_check("repack_kernel");
 }
 
+size_t st_int8_tiled_bytes(int K, int N) {
+    if (K <= 0 || N <= 0) return 0;
+    return (size_t)((N + kTileN - 1) / kTileN) * kTileN * (size_t)K;
+}
+
+int st_int8_repack(st_context *ctx, const int8_t *w, int8_t *w_tiled, int K, int N) {
+    if (!ctx || !w || !w_tiled) return st::fail(ST_ERR_INVALID, "st_int8_repack: NULL argument");
+    if (K <= 0 || K % 128 || N <= 0) return st::fail(ST_ERR_SHAPE, "st_int8_repack: K=%d (multiple of 128), N=%d", K, N);
+    if (!st::aligned16(w) || !st::aligned16(w_tiled))
+        return st::fail(ST_ERR_ALIGN, "st_int8_repack: w and w_tiled must be 16-byte aligned");
+    const int ntiles = (N + kTileN - 1) / kTileN;
+    const long long total = (long long)ntiles * (K / 128) * 128;
+    hipLaunchKernelGGL(repack8_kernel, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, ctx->stream, w, w_tiled, K,
+                       N, ntiles);
+    return st::launch_check("repack8_kernel");
+}
+
 int st_int8_matvec(st_context *ctx, const void *x, int x_dtype, const int8_t *w, const float *scale, float *y, int M,
-                   int K, int N) {
+                   int K, int N, uint32_t flags) {
     if (!ctx || !x || !w || !scale || !y) return st::fail(ST_ERR_INVALID, "st_int8_matvec: NULL argument");
     if (M < 1 || M > 32) return st::fail(ST_ERR_SHAPE, "st_int8_matvec: M=%d not in [1,32]", M);
     if (K <= 0 || K % 128) return st::fail(ST_ERR_SHAPE, "st_int8_matvec: K=%d not a positive multiple of 128", K);
     if (N <= 0 || N % 4) return st::fail(ST_ERR_SHAPE, "st_int8_matvec: N=%d not a positive multiple of 4", N);
-    if ((long long)N * K >= (1ll << 31))  // 32-bit buffer offsets
+    const bool tiled = (flags & ST_FLAG_TILED) != 0;
+    if ((long long)((N + kTileN - 1) / kTileN) * kTileN * K >= (1ll << 31))  // 32-bit buffer offsets
         return st::fail(ST_ERR_SHAPE, "st_int8_matvec: weight of %d x %d exceeds 2 GiB", N, K);
     if (!st::aligned16(w) || !st::aligned16(x))
         return st::fail(ST_ERR_ALIGN, "st_int8_matvec: w and x must be 16-byte aligned");
@@ -219,7 +258,9 @@ int st_int8_matvec(st_context *ctx, const void *x, int x_dtype, const int8_t *w,
     p.units = K / 128;
     p.ntiles = (N + kTileN - 1) / kTileN;
     const int xm = x_dtype == ST_F32 ? XM_F32 : XM_F16;
-    return by_token_blocks(p, xm, [&](QmvParams &q) { return dispatch<FMT_I8, false>(ctx, q, 1, xm); });
+    return by_token_blocks(p, xm, [&](QmvParams &q) {
+        return tiled ? dispatch<FMT_I8T, false>(ctx, q, 1, xm) : dispatch<FMT_I8, false>(ctx, q, 1, xm);
+    });
 }
 
 }  // extern "C"

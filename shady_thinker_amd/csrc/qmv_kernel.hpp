@@ -73,7 +73,9 @@ constexpr unsigned kNoLoad = 0x80000000u;
 constexpr int kNt = 2;  // buffer-load cache policy: non-temporal (streamed once)
 constexpr int kMaxZeroUnits = 64;  // groups per wave whose zero points fit the LDS table
 
-enum Fmt { FMT_I4 = 0, FMT_I4T = 1, FMT_I8 = 2 };
+enum Fmt { FMT_I4 = 0, FMT_I4T = 1, FMT_I8 = 2, FMT_I8T = 3 };
+// INT8 weights, row-major [N, K] (FMT_I8) or tiled (FMT_I8T, st_int8_repack)
+constexpr bool is_i8(int fmt) { return fmt == FMT_I8 || fmt == FMT_I8T; }
 enum XMode { XM_F32 = 0, XM_F16 = 1, XM_SILU = 2 };
 
 struct Params {
@@ -235,10 +237,10 @@ constexpr int kScaleUnits = 16;  // groups per wave covered by the COOP scale bl
 // (3 waves per SIMD, so every gate/up tile of a 7B layer is resident at once).
 template <int FMT, int NSRC, int SPU, bool COOP>
 constexpr int ring_depth() {
-    constexpr int WPU = (FMT == FMT_I8) ? 4 * SPU : 2 * SPU;
+    constexpr int WPU = (is_i8(FMT)) ? 4 * SPU : 2 * SPU;
     // (COOP keeps the depth it had with the scale in the ring: rings of 6
     // and 8 measured slower, more registers and more loads queued at issue)
-    constexpr int RPU = NSRC * (WPU + (FMT == FMT_I8 ? 0 : 1));
+    constexpr int RPU = NSRC * (WPU + (is_i8(FMT) ? 0 : 1));
     constexpr int budget = (COOP && NSRC == 2) ? 40 : 24;
     return (budget / RPU) < 2 ? 2 : ((budget / RPU) > 6 ? 6 : (budget / RPU));
 }
@@ -255,11 +257,11 @@ __global__ __launch_bounds__((64 * kMaxWavesFor<NSRC, (CM != 0)>)) void qmv_kern
     constexpr int D = CHK ? kChunkSlots : ring_depth<FMT, NSRC, SPU, COOP>();
     constexpr int DPRE = kRingBeforeBarrier < D ? kRingBeforeBarrier : D;  // COOP: slots before the barrier
     constexpr int IPU = 4 * SPU;                              // 16-k items per group and token
-    constexpr int WPU = (FMT == FMT_I8) ? 4 * SPU : 2 * SPU;  // weight dwords per lane per group
+    constexpr int WPU = (is_i8(FMT)) ? 4 * SPU : 2 * SPU;  // weight dwords per lane per group
     // staging rounds per lane: per-wave chunk (fallback) or whole slice (COOP)
     constexpr int RMAX = CHK ? kChunkRounds : (COOP ? kCoopRounds : (4 * MB * IPU + 63) / 64);
 
-    constexpr bool SCB = (CM == 1 || CM == 2) && FMT != FMT_I8;  // per-wave scale block (see below)
+    constexpr bool SCB = (CM == 1 || CM == 2) && !is_i8(FMT);  // per-wave scale block (see below)
     const int tid = threadIdx.x;
     const int lane = tid & 63;
     const int wave = tid >> 6;
@@ -322,8 +324,8 @@ __global__ __launch_bounds__((64 * kMaxWavesFor<NSRC, (CM != 0)>)) void qmv_kern
     // ------------------------------------------- zero points (before all loads)
     bool have_z[NSRC];
 #pragma unroll
-    for (int src = 0; src < NSRC; ++src) have_z[src] = FMT != FMT_I8 && p.qz[src] != nullptr;
-    if constexpr (FMT != FMT_I8) {
+    for (int src = 0; src < NSRC; ++src) have_z[src] = !is_i8(FMT) && p.qz[src] != nullptr;
+    if constexpr (!is_i8(FMT)) {
         if (have_z[0]) {
             // [tile slot][unit][src][column]; PW: each wave its own tile and groups
             const int nz = PW ? (u1 - u0) * NSRC * 16 : TB * ZU * NSRC * 16;
@@ -380,6 +382,18 @@ __global__ __launch_bounds__((64 * kMaxWavesFor<NSRC, (CM != 0)>)) void qmv_kern
                         U.w[src][j + 3] = t.w;
                     }
                 }
+            } else if constexpr (FMT == FMT_I8T) {
+                // tile T, group u, lane (q, c): 32 contiguous bytes, k = 128 u
+                // + 16 q + 64 st + j (st_int8_repack); a wave reads 2 KiB
+                const unsigned off = live ? (unsigned)(((tile * p.units + u) * 64 + lane) * 32) : kNoLoad;
+#pragma unroll
+                for (int st = 0; st < SPU; ++st) {
+                    const u32x4 t = __builtin_amdgcn_raw_buffer_load_b128(rw8, off + 16 * st, 0, kNt);
+                    U.w[src][4 * st] = t.x;
+                    U.w[src][4 * st + 1] = t.y;
+                    U.w[src][4 * st + 2] = t.z;
+                    U.w[src][4 * st + 3] = t.w;
+                }
             } else {
                 const unsigned off = live ? (unsigned)(ncol * K + u * 128 + 16 * q) : kNoLoad;
 #pragma unroll
@@ -391,7 +405,7 @@ __global__ __launch_bounds__((64 * kMaxWavesFor<NSRC, (CM != 0)>)) void qmv_kern
                     U.w[src][4 * st + 3] = t.w;
                 }
             }
-            if constexpr (FMT != FMT_I8 && !SCB) U.s[src] = p.sc[src][(size_t)u * N + ncol];
+            if constexpr (!is_i8(FMT) && !SCB) U.s[src] = p.sc[src][(size_t)u * N + ncol];
         }
     };
 
@@ -485,7 +499,7 @@ __global__ __launch_bounds__((64 * kMaxWavesFor<NSRC, (CM != 0)>)) void qmv_kern
                 u32x4 L2v, L1v, L0v;
 #pragma unroll
                 for (int rr = 0; rr < 4; ++rr) {
-                    constexpr bool nat = FMT == FMT_I8;
+                    constexpr bool nat = is_i8(FMT);
                     const unsigned a = Z[nat ? 4 * rr : i4_koff(4 * rr)];
                     const unsigned bb = Z[nat ? 4 * rr + 1 : i4_koff(4 * rr + 1)];
                     const unsigned cc = Z[nat ? 4 * rr + 2 : i4_koff(4 * rr + 2)];
@@ -553,7 +567,7 @@ __global__ __launch_bounds__((64 * kMaxWavesFor<NSRC, (CM != 0)>)) void qmv_kern
 #pragma unroll
             for (int src = 0; src < NSRC; ++src) {
                 v4i Bf;
-                if constexpr (FMT == FMT_I8) {
+                if constexpr (is_i8(FMT)) {
                     Bf = v4i{(int)U.w[src][4 * st], (int)U.w[src][4 * st + 1], (int)U.w[src][4 * st + 2],
                              (int)U.w[src][4 * st + 3]};
                 } else {
@@ -578,7 +592,7 @@ __global__ __launch_bounds__((64 * kMaxWavesFor<NSRC, (CM != 0)>)) void qmv_kern
                 const v4i S = acc[src][mb];
                 float f;
                 int z = 0;
-                if constexpr (FMT == FMT_I8) {
+                if constexpr (is_i8(FMT)) {
                     f = em;
                 } else {
                     const uint16_t sh = SCB ? s_sc[(wave * NSRC + src) * 256 + (u - u0) * 16 + c] : U.s[src];
@@ -763,7 +777,7 @@ __global__ __launch_bounds__((64 * kMaxWavesFor<NSRC, (CM != 0)>)) void qmv_kern
         if (m >= M || n >= N) continue;
         float out = v[0];
         if constexpr (NSRC == 2) out = silu_f(v[0]) * v[1];
-        if constexpr (FMT == FMT_I8) out *= p.scale8[n];
+        if constexpr (is_i8(FMT)) out *= p.scale8[n];
         p.y[(size_t)m * N + n] = out;
     }
 }
@@ -780,7 +794,7 @@ inline int mb_for(int M) { return M <= 4 ? 1 : (M <= 8 ? 2 : (M <= 16 ? 4 : 8));
 // Bytes of one staged group (A operands, scalars, zero table row).
 template <int FMT, int NSRC, int MB, int SPU>
 inline size_t unit_bytes(const Params &p) {
-    return (size_t)SPU * MB * 4 * p.rb * 16 + (size_t)p.M * 12 + (FMT == FMT_I8 ? 0 : (size_t)NSRC * 16);
+    return (size_t)SPU * MB * 4 * p.rb * 16 + (size_t)p.M * 12 + (is_i8(FMT) ? 0 : (size_t)NSRC * 16);
 }
 
 template <int FMT, int NSRC, int XM, int MB, int SPU, bool PERM, int CM>
@@ -812,9 +826,9 @@ int launch_t(st_context *ctx, Params &p) {
         auto try_coop = [&](int nw, int tpw, int grid) -> int {
             const size_t ub = unit_bytes<FMT, NSRC, MB, SPU>(p);
             const size_t region =
-                (ub * p.units + (FMT != FMT_I8 ? (size_t)(tpw - 1) * p.units * NSRC * 16 : 0) + 15) & ~size_t(15);
+                (ub * p.units + (!is_i8(FMT) ? (size_t)(tpw - 1) * p.units * NSRC * 16 : 0) + 15) & ~size_t(15);
             const size_t lds = region + (size_t)nw * NSRC * MB * 64 * sizeof(float) +
-                               (FMT != FMT_I8 ? (size_t)nw * NSRC * 128 * sizeof(unsigned) : 0);
+                               (!is_i8(FMT) ? (size_t)nw * NSRC * 128 * sizeof(unsigned) : 0);
             if (lds > kCoopLdsBudget) return -1;
             p.nwaves = nw;
             p.tpw = tpw;
@@ -835,7 +849,7 @@ int launch_t(st_context *ctx, Params &p) {
                     const long long ns = (items + 64 * rounds - 1) / (64 * rounds);
                     const long long wpt = (nw - ns) / tpw;  // compute waves per tile in the fullest workgroup
                     if (wpt < 1) continue;
-                    if (FMT != FMT_I8 && (p.units + wpt - 1) / wpt > kScaleUnits) continue;  // the scale block
+                    if (!is_i8(FMT) && (p.units + wpt - 1) / wpt > kScaleUnits) continue;  // the scale block
                     p.nstage = (int)ns;
                     return launch_kernel<FMT, NSRC, XM, MB, SPU, PERM, 1>(ctx, p, lds);
                 }
@@ -844,7 +858,7 @@ int launch_t(st_context *ctx, Params &p) {
             const int wpt = nw / tpw;
             if (wpt < 1) return -1;
             const int upw = (p.units + wpt - 1) / wpt;  // groups per wave
-            if (FMT != FMT_I8 && upw > kScaleUnits) return -1;
+            if (!is_i8(FMT) && upw > kScaleUnits) return -1;
             if ((long long)p.M * upw * IPU > 64ll * kCoopRounds) return -1;  // its staging rounds
             p.nstage = 0;
             return launch_kernel<FMT, NSRC, XM, MB, SPU, PERM, 2>(ctx, p, lds);
@@ -890,7 +904,7 @@ int launch_t(st_context *ctx, Params &p) {
             const int ch = wpt * kChunkSlots;
             const size_t a_bytes = (size_t)ch * ((size_t)SPU * MB * 4 * p.rb * 16 + (size_t)p.M * 12);
             const size_t region =
-                (a_bytes + (FMT != FMT_I8 ? (size_t)tpw * p.units * NSRC * 16 : 0) + 15) & ~size_t(15);
+                (a_bytes + (!is_i8(FMT) ? (size_t)tpw * p.units * NSRC * 16 : 0) + 15) & ~size_t(15);
             const size_t lds = region + (size_t)nw * NSRC * MB * 64 * sizeof(float);
             if ((long long)p.ntiles * grid < (1ll << 31) && wpt >= 1 &&
                 (long long)p.M * ch * IPU <= 64ll * kChunkRounds * nw && lds <= kChunkLdsBudget) {
@@ -910,10 +924,10 @@ int launch_t(st_context *ctx, Params &p) {
     p.tpw = 1;
     p.grid = p.ntiles;
     const int max_units = (p.units + nw - 1) / nw;
-    if (FMT != FMT_I8 && max_units > kMaxZeroUnits && (p.qz[0] || p.qz[1]))
+    if (!is_i8(FMT) && max_units > kMaxZeroUnits && (p.qz[0] || p.qz[1]))
         return fail(ST_ERR_SHAPE, "qmv: %d groups per wave exceed the zero-point table", max_units);
     const int afr = p.chunk * SPU * MB * 4 * p.rb;
-    const int ztab = (FMT == FMT_I8) ? 0 : std::min(max_units, kMaxZeroUnits) * NSRC * 16;
+    const int ztab = (is_i8(FMT)) ? 0 : std::min(max_units, kMaxZeroUnits) * NSRC * 16;
     p.wave_lds = (afr * 16 + p.chunk * p.M * 12 + ztab + 15) & ~15;
     const size_t lds = (size_t)nw * p.wave_lds + (size_t)nw * NSRC * MB * 64 * sizeof(float);
     return launch_kernel<FMT, NSRC, XM, MB, SPU, PERM, 0>(ctx, p, lds);
@@ -933,7 +947,7 @@ int launch_mb(st_context *ctx, Params &p) {
 
 template <int FMT, int NSRC, int XM, bool PERM>
 int launch_gs(st_context *ctx, Params &p) {
-    if constexpr (FMT == FMT_I8) {
+    if constexpr (is_i8(FMT)) {
         return launch_mb<FMT, NSRC, XM, 2, PERM>(ctx, p);
     } else {
         switch (p.gs) {
@@ -946,14 +960,14 @@ int launch_gs(st_context *ctx, Params &p) {
 }
 
 // Entry used by qmv.hip; specialised per (format, act-order) in
-// qmv_i4_p{0,1}.hip, qmv_i4t_p{0,1}.hip and qmv_i8.hip so the variants
-// compile in parallel.
+// qmv_i4_p{0,1}.hip, qmv_i4t_p{0,1}.hip, qmv_i8.hip and qmv_i8t.hip so the
+// variants compile in parallel.
 template <int FMT, bool PERM>
 int dispatch(st_context *ctx, Params &p, int nsrc, int xm);
 
 template <int FMT, bool PERM>
 int dispatch_impl(st_context *ctx, Params &p, int nsrc, int xm) {
-    if constexpr (FMT == FMT_I8) {
+    if constexpr (is_i8(FMT)) {
         if (xm == XM_F32) return launch_gs<FMT, 1, XM_F32, false>(ctx, p);
         return launch_gs<FMT, 1, XM_F16, false>(ctx, p);
     } else {

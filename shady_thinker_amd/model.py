@@ -76,11 +76,12 @@ def gptq_dequant(gpu, qweight, scales, out, k: int, n: int, group_size: int = 12
          group_size, flags)
 
 
-def int8_matvec(gpu, x, w, scale, y, k: int, n: int) -> None:
-    """y[M, n] = x[M, k] . (w[n, k]^T * scale[n]) (INT8 per-channel)."""
+def int8_matvec(gpu, x, w, scale, y, k: int, n: int, flags: int = 0) -> None:
+    """y[M, n] = x[M, k] . (w[n, k]^T * scale[n]) (INT8 per-channel); flags
+    ST_FLAG_TILED when w is in the layout of st_int8_repack."""
     m = _rows(x, k)
     gpu.sync_stream()
-    call("st_int8_matvec", gpu.handle, ptr(x), _xdtype(x), ptr(w), ptr(scale), ptr(y), m, k, n)
+    call("st_int8_matvec", gpu.handle, ptr(x), _xdtype(x), ptr(w), ptr(scale), ptr(y), m, k, n, flags)
 
 
 def gptq_gemm(gpu, a, qweight, scales, c, k: int, n: int, group_size: int = 128, qzeros=None, perm=None,

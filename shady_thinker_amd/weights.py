@@ -154,20 +154,29 @@ class GptqWeight:
 
 @dataclass
 class Int8Weight:
-    """INT8 symmetric per-output-channel weight: w int8 [N, K], scale f32 [N]."""
+    """INT8 symmetric per-output-channel weight: w int8 [N, K] row-major or,
+    with ST_FLAG_TILED in flags, the tiled layout of st_int8_repack; scale
+    f32 [N]."""
 
     w: object
     scale: object
     K: int
     N: int
+    flags: int = 0
 
     @classmethod
-    def upload(cls, gpu, w: np.ndarray, scale: np.ndarray) -> "Int8Weight":
+    def upload(cls, gpu, w: np.ndarray, scale: np.ndarray, tiled: bool = True) -> "Int8Weight":
         torch = gpu.torch
         w = np.ascontiguousarray(w, dtype=np.int8)
         N, K = w.shape
-        return cls(gpu.upload_array(w, torch.int8),
-                   gpu.upload_array(np.ascontiguousarray(scale, dtype=np.float32), torch.float32), K, N)
+        d_w = gpu.upload_array(w, torch.int8)
+        flags = 0
+        if tiled:
+            d_t = torch.empty(lib().st_int8_tiled_bytes(K, N), dtype=torch.int8, device=gpu.device)
+            gpu.sync_stream()
+            call("st_int8_repack", gpu.handle, d_w.data_ptr(), d_t.data_ptr(), K, N)
+            d_w, flags = d_t, ST_FLAG_TILED
+        return cls(d_w, gpu.upload_array(np.ascontiguousarray(scale, dtype=np.float32), torch.float32), K, N, flags)
 
     @property
     def nbytes(self) -> int:

@@ -199,7 +199,7 @@ def test_int8_cfg3(gpu, orc, Mr):
     w = sta.Int8Weight.upload(gpu, c["w"], c["scale"])
     x = torch.from_numpy(c["x"]).cuda()
     y = torch.empty(Mr, N, device="cuda")
-    M.int8_matvec(gpu, x, w.w, w.scale, y, K, N)
+    M.int8_matvec(gpu, x, w.w, w.scale, y, K, N, w.flags)
     torch.cuda.synchronize()
     ref = orc.int8_matvec_f64(c["x"], c["w"], c["scale"], K, N)
     e = orc.rel_l2(y.cpu().numpy(), ref)
@@ -212,7 +212,7 @@ def test_int8_f32_small_ragged(gpu, orc):
     c = orc.int8_case(82, K, N, M=3, x_dtype=np.float32)
     w = sta.Int8Weight.upload(gpu, c["w"], c["scale"])
     y = torch.empty(3, N, device="cuda")
-    M.int8_matvec(gpu, torch.from_numpy(c["x"]).cuda(), w.w, w.scale, y, K, N)
+    M.int8_matvec(gpu, torch.from_numpy(c["x"]).cuda(), w.w, w.scale, y, K, N, w.flags)
     torch.cuda.synchronize()
     assert orc.rel_l2(y.cpu().numpy(), orc.int8_matvec_f64(c["x"], c["w"], c["scale"], K, N)) < TOL
 
@@ -227,7 +227,7 @@ def test_golden_fixtures(gpu, orc):
             w = sta.Int8Weight.upload(gpu, d["w"], d["scale"])
             x = torch.from_numpy(d["x"]).cuda()
             y = torch.empty(d["y"].shape, device="cuda")
-            M.int8_matvec(gpu, x, w.w, w.scale, y, K, N)
+            M.int8_matvec(gpu, x, w.w, w.scale, y, K, N, w.flags)
         else:
             gs = int(d["gs"])
             w = sta.GptqWeight.upload(gpu, d["qweight"], d["scales"], gs,
@@ -461,3 +461,38 @@ def test_gate_up_multi_token_chunked_with_zeros(gpu, orc):
     assert orc.rel_l2(y, ref) < TOL
     for m in range(Mr):
         assert orc.rel_l2(y[m], ref[m]) < TOL
+
+
+def test_int8_repack_layout(gpu, orc):
+    """st_int8_repack: tile T, group u, lane (q, c) holds bytes k = 128 u +
+    16 q + 64 st + j of row 16 T + c (rows past N repeat row N - 1)."""
+    K, N = 384, 40
+    c = orc.int8_case(83, K, N)
+    w = sta.Int8Weight.upload(gpu, c["w"], c["scale"])
+    got = w.w.cpu().numpy().reshape(3, K // 128, 64, 2, 16)  # [tile][group][lane][st][16 bytes]
+    src = np.asarray(c["w"], np.int8)
+    for T in range(3):
+        for u in range(K // 128):
+            for lane in range(64):
+                n = min(16 * T + lane % 16, N - 1)
+                for st in range(2):
+                    k0 = 128 * u + 16 * (lane // 16) + 64 * st
+                    assert np.array_equal(got[T, u, lane, st], src[n, k0:k0 + 16])
+
+
+@pytest.mark.parametrize("Mr", [1, 3, 8, 16, 32])
+def test_int8_tiled_equals_row_major(gpu, orc, Mr):
+    """Tiled and row-major INT8 weights give the same y bit for bit (the same
+    integer products in the same order), within the bar of the f64 oracle."""
+    K, N = 5120, 4104
+    c = orc.int8_case(84 + Mr, K, N, M=Mr)
+    x = torch.from_numpy(c["x"]).cuda()
+    ys = []
+    for tiled in (True, False):
+        w = sta.Int8Weight.upload(gpu, c["w"], c["scale"], tiled=tiled)
+        y = torch.empty(Mr, N, device="cuda")
+        M.int8_matvec(gpu, x, w.w, w.scale, y, K, N, w.flags)
+        torch.cuda.synchronize()
+        ys.append(y.cpu().numpy())
+    assert np.array_equal(ys[0], ys[1])
+    assert orc.rel_l2(ys[0], orc.int8_matvec_f64(c["x"], c["w"], c["scale"], K, N)) < TOL
