@@ -869,6 +869,8 @@ int launch_t(st_context *ctx, Params &p) {
             if (tiles_cu >= 2 && !env_int("ST_QMV_ONE_TILE", 0)) {
                 // more tiles than CUs: a workgroup per CU (all the waves a CU
                 // holds) owns 2..kMaxTilesPerWg tiles and stages x once for them
+                // (every CU: a grid of ceil(ntiles / 3) even workgroups for
+                // gate/up measured 11.9 against 11.2 us)
                 const int grid = tiles_cu <= kMaxTilesPerWg ? ncu : (p.ntiles + kMaxTilesPerWg - 1) / kMaxTilesPerWg;
                 if ((long long)p.ntiles * grid < (1ll << 31)) {
                     const int rc = try_coop(NWX, (p.ntiles + grid - 1) / grid, grid);
