@@ -106,6 +106,8 @@ struct Params {
     int tpw;       // COOP: most tiles one workgroup owns (LDS zero table rows)
     int grid;      // workgroups
     int nstage;    // COOP: staging waves (they load no weights)
+    int ksplit;    // CHK: K slices (1 = none); > 1 writes f32 partials to part
+    float *part;   // CHK split: [ksplit][NSRC][M][N] partial sums (before the epilogue)
 };
 
 // silu(v) = v / (1 + exp(-v)) (fused_silu_gptq.wgsl:19-21), with the hardware
@@ -282,8 +284,12 @@ __global__ __launch_bounds__((64 * kMaxWavesFor<NSRC, (CM != 0)>)) void qmv_kern
     // N has more tiles than the grid has workgroups, so x is staged once for
     // them all); compute wave cw serves tile t0 + cw % TB, K slice cw / TB.
     // Fallback: one tile per workgroup.
-    const int b = blockIdx.x;
-    const int G = gridDim.x;
+    // CHK split-K: workgroup blockIdx.x = ksp * G + b takes K slice ksp of
+    // tile group b
+    const int KS = CHK ? p.ksplit : 1;
+    const int G = gridDim.x / KS;
+    const int b = blockIdx.x % G;
+    const int ksp = blockIdx.x / G;
     const int r_wg = (G % 8 == 0) ? (b % 8) * (G / 8) + b / 8 : b;
     // (32-bit divisions: the host keeps ntiles * G below 2^31 when G < ntiles)
     const bool multi = COOP && G != p.ntiles;
@@ -305,6 +311,9 @@ __global__ __launch_bounds__((64 * kMaxWavesFor<NSRC, (CM != 0)>)) void qmv_kern
     const int n0 = tile * kTileN;
     const int ncol = min(n0 + c, N - 1);  // clamped column this lane loads
 
+    // CHK: this workgroup's K slice of groups [ku0, ku1)
+    const int ku0 = CHK ? (int)((unsigned)(ksp * p.units) / (unsigned)KS) : 0;
+    const int ku1 = CHK ? (int)((unsigned)((ksp + 1) * p.units) / (unsigned)KS) : p.units;
     // contiguous K slice [u0, u1) (CHK: none; see its loop)
     const int u0 = (ks < WPT && !CHK) ? (int)((unsigned)(ks * p.units) / (unsigned)WPT) : 0;
     const int u1 = (ks < WPT && !CHK) ? (int)((unsigned)((ks + 1) * p.units) / (unsigned)WPT) : 0;
@@ -333,11 +342,14 @@ __global__ __launch_bounds__((64 * kMaxWavesFor<NSRC, (CM != 0)>)) void qmv_kern
     for (int src = 0; src < NSRC; ++src) have_z[src] = !is_i8(FMT) && p.qz[src] != nullptr;
     if constexpr (!is_i8(FMT)) {
         if (have_z[0]) {
-            // [tile slot][unit][src][column]; PW: each wave its own tile and groups
-            const int nz = PW ? (u1 - u0) * NSRC * 16 : TB * ZU * NSRC * 16;
+            // [tile slot][unit][src][column]; PW: each wave its own tile and
+            // groups; CHK: the workgroup's K slice [ku0, ku1) of every tile
+            const int zs = CHK ? ku1 - ku0 : ZU;  // units filled per tile
+            const int nz = PW ? (u1 - u0) * NSRC * 16 : TB * zs * NSRC * 16;
             const int first = (COOP && !PW) ? tid : lane, stride = (COOP && !PW) ? 64 * NW : 64;
             for (int i0 = first; i0 < nz; i0 += stride) {
-                const int i = PW ? (tj * ZU + u0) * NSRC * 16 + i0 : i0;
+                const int i = PW ? (tj * ZU + u0) * NSRC * 16 + i0
+                                 : (CHK ? ((i0 / (zs * NSRC * 16)) * ZU + ku0) * NSRC * 16 + i0 % (zs * NSRC * 16) : i0);
                 const int col = i & 15, src = (i >> 4) % NSRC, uz = (i / (16 * NSRC)) % ZU, tz = i / (16 * NSRC * ZU);
                 const int zc = min((t0 + tz) * kTileN + col, N - 1);
                 const unsigned w = p.qz[src][(size_t)(zbase + uz) * (N >> 3) + (zc >> 3)];
@@ -631,11 +643,11 @@ __global__ __launch_bounds__((64 * kMaxWavesFor<NSRC, (CM != 0)>)) void qmv_kern
         // next chunk between two bare barriers (the ring stays in flight).
         // Every load is unconditional (the last chunk's x is loaded again
         // at the end; groups past K are empty slots).
-        const int nch = (p.units + CH - 1) / CH;
-        int cs = 0;
+        const int nch = (ku1 - ku0 + CH - 1) / CH;
+        int cs = ku0;
         auto set_chunk = [&](int cc) {
-            cs = cc * CH;
-            uend = min(cs + CH, p.units);
+            cs = ku0 + cc * CH;
+            uend = min(cs + CH, ku1);
             SW = uend - cs;
             items = M * SW * IPU;
         };
@@ -644,8 +656,8 @@ __global__ __launch_bounds__((64 * kMaxWavesFor<NSRC, (CM != 0)>)) void qmv_kern
         xload(cs);
 #pragma unroll
         for (int d = 0; d < D; ++d) {
-            const int u = ks * D + d;
-            load_unit(ring[d], min(u, p.units - 1), comp && u < p.units);
+            const int u = ku0 + ks * D + d;
+            load_unit(ring[d], min(u, ku1 - 1), comp && u < ku1);
         }
         stage(cs);
         asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
@@ -654,10 +666,10 @@ __global__ __launch_bounds__((64 * kMaxWavesFor<NSRC, (CM != 0)>)) void qmv_kern
             xload(cs);
 #pragma unroll
             for (int d = 0; d < D; ++d) {
-                const int u = cc * CH + ks * D + d;
-                if (comp && u < p.units) compute(ring[d], u, u - cc * CH);
+                const int u = ku0 + cc * CH + ks * D + d;
+                if (comp && u < ku1) compute(ring[d], u, u - ku0 - cc * CH);
                 const int un = u + CH;
-                load_unit(ring[d], min(un, p.units - 1), comp && cc + 1 < nch && un < p.units);
+                load_unit(ring[d], min(un, ku1 - 1), comp && cc + 1 < nch && un < ku1);
             }
             asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");  // chunk cc's A operands are free
             if (cc + 1 < nch) stage(cs);
@@ -781,11 +793,38 @@ __global__ __launch_bounds__((64 * kMaxWavesFor<NSRC, (CM != 0)>)) void qmv_kern
             v[src] = a;
         }
         if (m >= M || n >= N) continue;
+        if (KS > 1) {  // split-K partial: the reduce kernel applies the epilogue
+#pragma unroll
+            for (int src = 0; src < NSRC; ++src) p.part[(((size_t)ksp * NSRC + src) * M + m) * N + n] = v[src];
+            continue;
+        }
         float out = v[0];
         if constexpr (NSRC == 2) out = silu_f(v[0]) * v[1];
         if constexpr (is_i8(FMT)) out *= p.scale8[n];
         p.y[(size_t)m * N + n] = out;
     }
+}
+
+// CHK split-K: y[m, n] = epilogue(sum over s < S of part[s][src][m][n]), the
+// slices added in a fixed order (deterministic); the epilogue is the main
+// kernel's (silu(g) * u for two sources, the INT8 scale).
+template <int NSRC, bool I8>
+__global__ __launch_bounds__(256) void split_reduce_kernel(const float *__restrict__ part,
+                                                           const float *__restrict__ scale8, float *__restrict__ y,
+                                                           int M, int N, int S) {
+    const int idx = blockIdx.x * 256 + threadIdx.x;
+    const int MN = M * N;
+    if (idx >= MN) return;
+    float v[NSRC];
+#pragma unroll
+    for (int src = 0; src < NSRC; ++src) v[src] = 0.0f;
+    for (int s = 0; s < S; ++s)
+#pragma unroll
+        for (int src = 0; src < NSRC; ++src) v[src] += part[(size_t)(s * NSRC + src) * MN + idx];
+    float out = v[0];
+    if constexpr (NSRC == 2) out = silu_f(v[0]) * v[1];
+    if constexpr (I8) out *= scale8[idx % N];
+    y[idx] = out;
 }
 
 // ----------------------------------------------------------------- host side
@@ -814,6 +853,10 @@ int launch_kernel(st_context *ctx, Params &p, size_t lds) {
 
 constexpr size_t kCoopLdsBudget = 96 * 1024;
 constexpr size_t kChunkLdsBudget = 150 * 1024;  // one workgroup per CU
+constexpr int kSplitTiles = 4;  // CHK split-K: tiles per workgroup
+constexpr int kSplitTilesPerCu = 1;  // CHK: split K when the grid has at most this many tiles per CU
+constexpr int kSplitMinUnits1 = 48;  // CHK, one token block: split only K of at least this many groups
+constexpr int kMaxKSplit = 16;  // CHK split-K: most K slices
 
 template <int FMT, int NSRC, int XM, int MB, int SPU, bool PERM>
 int launch_t(st_context *ctx, Params &p) {
@@ -822,6 +865,64 @@ int launch_t(st_context *ctx, Params &p) {
     p.chunk = std::max(1, 64 / (p.M * IPU));
     // Waves per workgroup: aim at ~4 waves per SIMD over the whole grid
     // (each workgroup is one 16-column tile).
+    // Several tokens: K-chunked cooperative staging (CM 3). Many tiles (and
+    // several token blocks): a workgroup per CU owning 2..kMaxTilesPerWg
+    // tiles; few tiles (at most kSplitTilesPerCu per CU): groups of
+    // kSplitTiles tiles and K split across workgroups. One token block with
+    // many tiles goes to the single-block kernels below.
+    // (up to 16 tokens: calls with more run as 16-token blocks, and 8 token
+    // blocks would not fit the registers)
+    if constexpr (MB <= 4 && FMT != FMT_I4) {
+        constexpr int NWX = kMaxWavesFor<NSRC, true>;
+        const int ncu = std::max(1, ctx->num_cus);
+        const int tiles_cu = (p.ntiles + ncu - 1) / ncu;
+        // (measured, configs[4] shapes: one token block splits only a long K,
+        // down 17 -> 9.8 us at 4 tokens while o_proj, K = 4096, lost; four
+        // blocks split up to 2 tiles per CU, qkv 18.4 -> 16.7 us at 16)
+        const int split_max = env_int("ST_QMV_SPLIT_TILES_CU", MB >= 4 ? 2 : kSplitTilesPerCu);
+        const bool split = tiles_cu <= split_max && (MB > 1 || p.units >= kSplitMinUnits1);
+        if (p.M > 1 && (MB > 1 || split) && !env_int("ST_QMV_NO_CHUNK", 0)) {
+            int grid, tpw, ks = 1;
+            if (!split) {
+                grid = tiles_cu <= kMaxTilesPerWg ? ncu : (p.ntiles + kMaxTilesPerWg - 1) / kMaxTilesPerWg;
+                tpw = (p.ntiles + grid - 1) / grid;
+            } else {
+                // Fewer tiles than CUs: groups of kSplitTiles tiles share
+                // their x, and K is split into slices so that the grid fills
+                // the CUs (each slice stages only its part of x); f32
+                // partials in the workspace, then split_reduce_kernel.
+                tpw = std::min(kSplitTiles, p.ntiles);
+                grid = (p.ntiles + tpw - 1) / tpw;
+                ks = std::max(1, std::min({ncu / grid, kMaxKSplit, p.units / 2}));
+                if (env_int("ST_QMV_NO_KSPLIT", 0)) ks = 1;
+                const size_t need = (size_t)ks * NSRC * p.M * p.N * sizeof(float);
+                if (ks > 1 && (need > ctx->ws_bytes || !ctx->ws)) ks = 1;
+            }
+            const int nw = NWX, wpt = nw / tpw;
+            const int ch = wpt * kChunkSlots;
+            const size_t a_bytes = (size_t)ch * ((size_t)SPU * MB * 4 * p.rb * 16 + (size_t)p.M * 12);
+            const size_t region =
+                (a_bytes + (!is_i8(FMT) ? (size_t)tpw * p.units * NSRC * 16 : 0) + 15) & ~size_t(15);
+            const size_t lds = region + (size_t)nw * NSRC * MB * 64 * sizeof(float);
+            if ((long long)p.ntiles * grid < (1ll << 31) && wpt >= 1 &&
+                (long long)p.M * ch * IPU <= 64ll * kChunkRounds * nw && lds <= kChunkLdsBudget) {
+                p.nwaves = nw;
+                p.tpw = tpw;
+                p.grid = grid * ks;
+                p.chunk = ch;
+                p.nstage = 0;
+                p.wave_lds = (int)region;
+                p.ksplit = ks;
+                p.part = ks > 1 ? ctx->ws : nullptr;
+                if (int rc = launch_kernel<FMT, NSRC, XM, MB, SPU, PERM, 3>(ctx, p, lds)) return rc;
+                if (ks == 1) return ST_OK;
+                const int mn = p.M * p.N;
+                hipLaunchKernelGGL((split_reduce_kernel<NSRC, is_i8(FMT)>), dim3((mn + 255) / 256), dim3(256), 0,
+                                   ctx->stream, p.part, p.scale8, p.y, p.M, p.N, ks);
+                return launch_check("split_reduce_kernel");
+            }
+        }
+    }
     const int want = (ctx->num_cus * 16) / std::max(1, p.ntiles);
     if constexpr (MB == 1 && FMT != FMT_I4) {
         constexpr int NWX = kMaxWavesFor<NSRC, true>;
@@ -894,35 +995,6 @@ int launch_t(st_context *ctx, Params &p) {
                     if (rc != -1) return rc;
                     break;
                 }
-            }
-        }
-    }
-    // Several token blocks, more tiles than CUs: K-chunked cooperative
-    // staging (CM 3), a workgroup per CU owning 2..kMaxTilesPerWg tiles.
-    // (up to 16 tokens: calls with more run as 16-token blocks, and 8 token
-    // blocks would not fit the registers)
-    if constexpr (MB > 1 && MB <= 4 && FMT != FMT_I4) {
-        constexpr int NWX = kMaxWavesFor<NSRC, true>;
-        const int ncu = std::max(1, ctx->num_cus);
-        const int tiles_cu = (p.ntiles + ncu - 1) / ncu;
-        if (tiles_cu >= 2 && !env_int("ST_QMV_NO_CHUNK", 0)) {
-            const int grid = tiles_cu <= kMaxTilesPerWg ? ncu : (p.ntiles + kMaxTilesPerWg - 1) / kMaxTilesPerWg;
-            const int tpw = (p.ntiles + grid - 1) / grid;
-            const int nw = NWX, wpt = nw / tpw;
-            const int ch = wpt * kChunkSlots;
-            const size_t a_bytes = (size_t)ch * ((size_t)SPU * MB * 4 * p.rb * 16 + (size_t)p.M * 12);
-            const size_t region =
-                (a_bytes + (!is_i8(FMT) ? (size_t)tpw * p.units * NSRC * 16 : 0) + 15) & ~size_t(15);
-            const size_t lds = region + (size_t)nw * NSRC * MB * 64 * sizeof(float);
-            if ((long long)p.ntiles * grid < (1ll << 31) && wpt >= 1 &&
-                (long long)p.M * ch * IPU <= 64ll * kChunkRounds * nw && lds <= kChunkLdsBudget) {
-                p.nwaves = nw;
-                p.tpw = tpw;
-                p.grid = grid;
-                p.chunk = ch;
-                p.nstage = 0;
-                p.wave_lds = (int)region;
-                return launch_kernel<FMT, NSRC, XM, MB, SPU, PERM, 3>(ctx, p, lds);
             }
         }
     }

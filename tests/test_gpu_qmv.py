@@ -496,3 +496,52 @@ def test_int8_tiled_equals_row_major(gpu, orc, Mr):
         ys.append(y.cpu().numpy())
     assert np.array_equal(ys[0], ys[1])
     assert orc.rel_l2(ys[0], orc.int8_matvec_f64(c["x"], c["w"], c["scale"], K, N)) < TOL
+
+
+@pytest.mark.parametrize("kind,K,N,Mr", [
+    ("gptq", 9728, 2560, 16),   # configs[4] down at batch 16: 160 tiles, K split 6 ways
+    ("gptq", 4096, 520, 5),     # 33 tiles, ragged
+    ("dual", 2560, 1032, 12),   # gate/up with zeros
+    ("int8", 5120, 1024, 8),
+])
+def test_multi_token_split_k(gpu, orc, kind, K, N, Mr, monkeypatch):
+    """Fewer 16-column tiles than CUs, several tokens: K is split across
+    workgroups (f32 partials in the workspace, a fixed-order reduce that
+    applies the epilogue). Same values as without the split and as the
+    per-wave fallback, up to f32 summation order; the f64 oracle's bar."""
+    def run():
+        y = torch.empty(Mr, N, device="cuda")
+        if kind == "int8":
+            M.int8_matvec(gpu, x, w.w, w.scale, y, K, N, w.flags)
+        elif kind == "dual":
+            M.fused_gate_up_silu(gpu, x, w.qweight, w.scales, w2.qweight, w2.scales, y, K, N, 128,
+                                 gate_qz=w.qzeros, up_qz=w2.qzeros, flags=w.flags)
+        else:
+            M.gptq_matvec(gpu, "t", x, w.qweight, w.scales, y, K, N, 128, w.qzeros, w.perm, w.flags)
+        torch.cuda.synchronize()
+        return y.cpu().numpy()
+
+    if kind == "int8":
+        c = orc.int8_case(100 + Mr, K, N, M=Mr)
+        w = sta.Int8Weight.upload(gpu, c["w"], c["scale"])
+        ref = orc.int8_matvec_f64(c["x"], c["w"], c["scale"], K, N)
+    else:
+        c = orc.gptq_case(100 + Mr, K, N, 128, zeros=True, act_order=(kind == "gptq"), M=Mr)
+        w = up(gpu, c)
+        ref = orc.gptq_matvec_f64(c["x"], c["qweight"], c["scales"], K, N, 128, qzeros=c["qzeros"], g_idx=c["g_idx"])
+        if kind == "dual":
+            c2 = orc.gptq_case(200 + Mr, K, N, 128, zeros=True)
+            w2 = up(gpu, c2)
+            u = orc.gptq_matvec_f64(c["x"], c2["qweight"], c2["scales"], K, N, 128, qzeros=c2["qzeros"])
+            ref = orc.silu_gate_f64(ref, u)
+    x = torch.from_numpy(c["x"]).cuda()
+    y = run()
+    monkeypatch.setenv("ST_QMV_NO_KSPLIT", "1")
+    y1 = run()
+    monkeypatch.setenv("ST_QMV_NO_CHUNK", "1")
+    y0 = run()
+    e = orc.rel_l2(y, ref)
+    print(f"split-K {kind} K={K} N={N} M={Mr}: rel-L2 {e:.3e}, vs unsplit {orc.rel_l2(y, y1):.3e}, vs fallback {orc.rel_l2(y, y0):.3e}")
+    assert e < TOL and orc.rel_l2(y, y1) < 1e-6 and orc.rel_l2(y, y0) < 1e-6
+    for m in range(Mr):
+        assert orc.rel_l2(y[m], ref[m]) < TOL
