@@ -237,7 +237,19 @@ constexpr int kCoopRounds = 4;  // x staging rounds per staging wave in COOP ker
 // CHK kernels: consecutive groups per wave per K chunk (the ring depth); 3
 // and 4 measured slower (32 INT8 tokens: 84 and 119 against 65 us)
 constexpr int kChunkSlots = 2;
-constexpr int kChunkRounds = 2;  // CHK kernels: x staging rounds per wave per chunk
+// CHK kernels: x staging rounds per wave per chunk. One for one source (16
+// waves cover a chunk of 16 tokens in one round): the next chunk's x is held
+// in registers across the compute, and a second round made the 16-token
+// kernels spill (each spill reload is a scratch load, whose wait drains
+// every load in flight).
+template <int NSRC>
+constexpr int kChunkRounds = NSRC == 1 ? 1 : 2;
+// CHK kernels: waves per workgroup. Four token blocks (16 tokens) take
+// fewer than the other cooperative kernels so that they fit the registers
+// without spills (at most 170 VGPRs with 12 waves, 256 with 8); fewer
+// blocks keep 16 / 12.
+template <int NSRC, int MB>
+constexpr int kChunkWaves = MB >= 4 ? (NSRC == 1 ? 12 : 8) : (NSRC == 1 ? 16 : 12);
 constexpr int kScaleUnits = 16;  // groups per wave covered by the COOP scale block (two loads per source)
 
 // Prefetch ring depth: the registers of weights in flight per lane, about 24
@@ -258,7 +270,7 @@ constexpr int ring_depth() {
 // cooperative in K chunks (several token blocks: all waves stage each chunk,
 // each wave computes kChunkSlots consecutive groups of every chunk).
 template <int FMT, int NSRC, int XM, int MB, int SPU, bool PERM, int CM>
-__global__ __launch_bounds__((64 * kMaxWavesFor<NSRC, (CM != 0)>)) void qmv_kernel(Params p) {
+__global__ __launch_bounds__((64 * (CM == 3 ? kChunkWaves<NSRC, MB> : kMaxWavesFor<NSRC, (CM != 0)>))) void qmv_kernel(Params p) {
     constexpr bool COOP = CM != 0;
     constexpr bool CHK = CM == 3;
     extern __shared__ __align__(16) unsigned char smem[];
@@ -267,7 +279,7 @@ __global__ __launch_bounds__((64 * kMaxWavesFor<NSRC, (CM != 0)>)) void qmv_kern
     constexpr int IPU = 4 * SPU;                              // 16-k items per group and token
     constexpr int WPU = (is_i8(FMT)) ? 4 * SPU : 2 * SPU;  // weight dwords per lane per group
     // staging rounds per lane: per-wave chunk (fallback) or whole slice (COOP)
-    constexpr int RMAX = CHK ? kChunkRounds : (COOP ? kCoopRounds : (4 * MB * IPU + 63) / 64);
+    constexpr int RMAX = CHK ? kChunkRounds<NSRC> : (COOP ? kCoopRounds : (4 * MB * IPU + 63) / 64);
 
     constexpr bool SCB = (CM == 1 || CM == 2) && !is_i8(FMT);  // per-wave scale block (see below)
     const int tid = threadIdx.x;
@@ -569,6 +581,7 @@ __global__ __launch_bounds__((64 * kMaxWavesFor<NSRC, (CM != 0)>)) void qmv_kern
 #pragma unroll
         for (int mb = 0; mb < MB; ++mb) tot[src][mb] = 0.0f;
 
+    const u32x4 *alane = abuf + q * RB + c;  // this lane's A operand of (unit 0, step 0, block 0)
     auto compute = [&](const Unit &U, int u, int ui) {
         v4i acc[NSRC][MB];
 #pragma unroll
@@ -578,10 +591,12 @@ __global__ __launch_bounds__((64 * kMaxWavesFor<NSRC, (CM != 0)>)) void qmv_kern
 #pragma unroll
         for (int st = 0; st < SPU; ++st) {
             v4i A[MB];
+            // (several token blocks: RB = 16, every lane reads; its address
+            // is the lane's base plus a constant per (st, mb))
 #pragma unroll
             for (int mb = 0; mb < MB; ++mb)
-                A[mb] = (c < RB) ? __builtin_bit_cast(v4i, abuf[(((size_t)(ui * SPU + st) * MB + mb) * 4 + q) * RB + c])
-                                 : v4i{0, 0, 0, 0};
+                A[mb] = (MB > 1 || c < RB) ? __builtin_bit_cast(v4i, alane[((ui * SPU + st) * MB + mb) * 4 * RB])
+                                           : v4i{0, 0, 0, 0};
 #pragma unroll
             for (int src = 0; src < NSRC; ++src) {
                 v4i Bf;
@@ -873,7 +888,6 @@ int launch_t(st_context *ctx, Params &p) {
     // (up to 16 tokens: calls with more run as 16-token blocks, and 8 token
     // blocks would not fit the registers)
     if constexpr (MB <= 4 && FMT != FMT_I4) {
-        constexpr int NWX = kMaxWavesFor<NSRC, true>;
         const int ncu = std::max(1, ctx->num_cus);
         const int tiles_cu = (p.ntiles + ncu - 1) / ncu;
         // (measured, configs[4] shapes: one token block splits only a long K,
@@ -900,14 +914,18 @@ int launch_t(st_context *ctx, Params &p) {
                 const size_t need = (size_t)ks * NSRC * p.M * p.N * sizeof(float);
                 if (ks > 1 && (need > ctx->ws_bytes || !ctx->ws)) ks = 1;
             }
-            const int nw = NWX, wpt = nw / tpw;
+            // compute waves per tile: as many as the waves allow, and no more
+            // than one chunk's staging (kChunkRounds rounds of all waves) covers
+            const int nw = kChunkWaves<NSRC, MB>;
+            const int cap = (int)(64ll * kChunkRounds<NSRC> * nw / ((long long)p.M * IPU * kChunkSlots));
+            const int wpt = std::min(nw / tpw, cap);
             const int ch = wpt * kChunkSlots;
             const size_t a_bytes = (size_t)ch * ((size_t)SPU * MB * 4 * p.rb * 16 + (size_t)p.M * 12);
             const size_t region =
                 (a_bytes + (!is_i8(FMT) ? (size_t)tpw * p.units * NSRC * 16 : 0) + 15) & ~size_t(15);
             const size_t lds = region + (size_t)nw * NSRC * MB * 64 * sizeof(float);
             if ((long long)p.ntiles * grid < (1ll << 31) && wpt >= 1 &&
-                (long long)p.M * ch * IPU <= 64ll * kChunkRounds * nw && lds <= kChunkLdsBudget) {
+                (long long)p.M * ch * IPU <= 64ll * kChunkRounds<NSRC> * nw && lds <= kChunkLdsBudget) {
                 p.nwaves = nw;
                 p.tpw = tpw;
                 p.grid = grid * ks;
