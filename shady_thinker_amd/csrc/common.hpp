@@ -16,13 +16,11 @@ struct st_context {
     hipStream_t stream = nullptr;
     bool own_stream = false;
     int num_cus = 256;
-    // Split-K workspace: per-split partial sums, and one arrival counter per
-    // column block. Counters are zeroed once here and reset to zero by the
-    // kernel that consumes them, so no per-call clearing is needed.
+    // Workspace: the prefill GEMM's pre-processed A and split-K partials,
+    // and the multi-token decode's split-K partials (each call overwrites
+    // what it uses; calls on one context are ordered by its stream).
     float *ws = nullptr;
     size_t ws_bytes = 0;
-    unsigned *counters = nullptr;
-    int n_counters = 0;
 };
 
 namespace st {

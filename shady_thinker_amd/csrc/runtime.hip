@@ -25,7 +25,6 @@ void clear_error() { g_last_error.clear(); }
 }  // namespace st
 
 static constexpr size_t kDefaultWorkspace = size_t(64) << 20;
-static constexpr int kCounters = 1 << 16;
 
 extern "C" {
 
@@ -55,17 +54,13 @@ int st_context_create(int device, st_context **out) {
         return st::hip_fail(e, "hipStreamCreateWithFlags");
     }
     ctx->own_stream = true;
-    e = hipMalloc(&ctx->counters, sizeof(unsigned) * kCounters);
-    if (e == hipSuccess) e = hipMemset(ctx->counters, 0, sizeof(unsigned) * kCounters);
-    if (e == hipSuccess) e = hipMalloc(&ctx->ws, kDefaultWorkspace);
+    e = hipMalloc(&ctx->ws, kDefaultWorkspace);
     if (e != hipSuccess) {
-        if (ctx->counters) (void)hipFree(ctx->counters);
         if (ctx->ws) (void)hipFree(ctx->ws);
         (void)hipStreamDestroy(ctx->stream);
         delete ctx;
         return st::hip_fail(e, "st_context_create: workspace");
     }
-    ctx->n_counters = kCounters;
     ctx->ws_bytes = kDefaultWorkspace;
     *out = ctx;
     st::clear_error();
@@ -109,7 +104,6 @@ int st_context_destroy(st_context *ctx) {
     (void)hipSetDevice(ctx->device);
     (void)hipStreamSynchronize(ctx->stream);
     if (ctx->ws) (void)hipFree(ctx->ws);
-    if (ctx->counters) (void)hipFree(ctx->counters);
     if (ctx->own_stream) (void)hipStreamDestroy(ctx->stream);
     delete ctx;
     return ST_OK;
