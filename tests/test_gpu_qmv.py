@@ -545,3 +545,52 @@ def test_multi_token_split_k(gpu, orc, kind, K, N, Mr, monkeypatch):
     assert e < TOL and orc.rel_l2(y, y1) < 1e-6 and orc.rel_l2(y, y0) < 1e-6
     for m in range(Mr):
         assert orc.rel_l2(y[m], ref[m]) < TOL
+
+
+def test_graph_replay_multi_token_split_k(gpu, orc):
+    """A captured multi-token call on a narrow linear (split-K partials in the
+    context workspace + reduce) and a multi-tile chunked call, replayed with a
+    different eager call that also uses the workspace in between: every replay
+    gives the eager result."""
+    Mr = 16
+    cd = orc.gptq_case(97, 9728, 2560, 128, M=Mr)       # 160 tiles: split K
+    wd = up(gpu, cd)
+    cq = orc.gptq_case(98, 2560, 8200, 128, M=Mr)       # 513 tiles: chunked, no split
+    wq = up(gpu, cq)
+    xd = torch.from_numpy(cd["x"]).cuda()
+    xq = torch.from_numpy(cq["x"]).cuda()
+    co = orc.gptq_case(99, 4096, 1032, 128, M=8)        # other split-K work between replays
+    wo = up(gpu, co)
+    xo = torch.from_numpy(co["x"]).cuda()
+    yo = torch.empty(8, 1032, device="cuda")
+
+    def calls(yd, yq):
+        M.gptq_matvec(gpu, "d", xd, wd.qweight, wd.scales, yd, 9728, 2560, 128, flags=wd.flags)
+        M.gptq_matvec(gpu, "q", xq, wq.qweight, wq.scales, yq, 2560, 8200, 128, flags=wq.flags)
+
+    yd_e = torch.empty(Mr, 2560, device="cuda")
+    yq_e = torch.empty(Mr, 8200, device="cuda")
+    calls(yd_e, yq_e)
+    torch.cuda.synchronize()
+    yd = torch.zeros_like(yd_e)
+    yq = torch.zeros_like(yq_e)
+    s = torch.cuda.Stream()
+    with torch.cuda.stream(s):
+        calls(yd, yq)  # warm on s
+        torch.cuda.synchronize()
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g, stream=s):
+            calls(yd, yq)
+    for rep in range(4):
+        yd.fill_(float("nan"))
+        yq.fill_(float("nan"))
+        torch.cuda.synchronize()
+        with torch.cuda.stream(s):
+            g.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(yd, yd_e), rep
+        assert torch.equal(yq, yq_e), rep
+        M.gptq_matvec(gpu, "o", xo, wo.qweight, wo.scales, yo, 4096, 1032, 128, flags=wo.flags)
+        torch.cuda.synchronize()
+    ref = orc.gptq_matvec_f64(cd["x"], cd["qweight"], cd["scales"], 9728, 2560, 128)
+    assert orc.rel_l2(yd.cpu().numpy(), ref) < TOL
