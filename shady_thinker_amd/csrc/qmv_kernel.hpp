@@ -340,10 +340,9 @@ __global__ __launch_bounds__((64 * (CM == 3 ? kChunkWaves<NSRC, MB> : kMaxWavesF
     unsigned char *region = smem + (COOP ? 0 : (size_t)wave * p.wave_lds);
     u32x4 *abuf = reinterpret_cast<u32x4 *>(region);
     const int afrags = CH * SPU * MB * 4 * RB;
-    float *s_em = reinterpret_cast<float *>(abuf + afrags);
-    int *s_nh = reinterpret_cast<int *>(s_em + CH * M);
-    int *s_nl = s_nh + CH * M;
-    unsigned char *s_z = reinterpret_cast<unsigned char *>(s_nl + CH * M);
+    // per (unit, token): {2^-e bits, -H, -L, 0}, one 16-byte read in the epilogue
+    u32x4 *s_es = abuf + afrags;
+    unsigned char *s_z = reinterpret_cast<unsigned char *>(s_es + CH * M);
     const int zbase = COOP ? 0 : u0;  // unit index of s_z row 0
     // COOP scale table: [wave][src][group - u0 (< kScaleUnits = 16)][16 columns], after the reduction area
     uint16_t *s_sc = reinterpret_cast<uint16_t *>(smem + (size_t)p.wave_lds + (size_t)NW * NSRC * MB * 64 * sizeof(float));
@@ -551,9 +550,8 @@ __global__ __launch_bounds__((64 * (CM == 3 ? kChunkWaves<NSRC, MB> : kMaxWavesF
                 dst[3] = u32x4{0, 0, 0, 0};  // row 4t+3 (see the zero fill below)
                 if (ii == 0) {
                     const int h = (sum + 32768) >> 16;
-                    s_em[ua * M + m] = em;
-                    s_nh[ua * M + m] = -h;
-                    s_nl[ua * M + m] = -(sum - (h << 16));
+                    s_es[ua * M + m] = u32x4{__builtin_bit_cast(unsigned, em), (unsigned)(-h),
+                                             (unsigned)(-(sum - (h << 16))), 0u};
                 }
             }
         }
@@ -618,8 +616,9 @@ __global__ __launch_bounds__((64 * (CM == 3 ? kChunkWaves<NSRC, MB> : kMaxWavesF
 #pragma unroll
         for (int mb = 0; mb < MB; ++mb) {
             const int m = min(mb * 4 + q, M - 1);
-            const float em = s_em[ui * M + m];
-            const int nh = s_nh[ui * M + m], nl = s_nl[ui * M + m];
+            const u32x4 es = s_es[ui * M + m];
+            const float em = __builtin_bit_cast(float, es.x);
+            const int nh = (int)es.y, nl = (int)es.z;
 #pragma unroll
             for (int src = 0; src < NSRC; ++src) {
                 const v4i S = acc[src][mb];
@@ -854,7 +853,7 @@ inline int mb_for(int M) { return M <= 4 ? 1 : (M <= 8 ? 2 : (M <= 16 ? 4 : 8));
 // Bytes of one staged group (A operands, scalars, zero table row).
 template <int FMT, int NSRC, int MB, int SPU>
 inline size_t unit_bytes(const Params &p) {
-    return (size_t)SPU * MB * 4 * p.rb * 16 + (size_t)p.M * 12 + (is_i8(FMT) ? 0 : (size_t)NSRC * 16);
+    return (size_t)SPU * MB * 4 * p.rb * 16 + (size_t)p.M * 16 + (is_i8(FMT) ? 0 : (size_t)NSRC * 16);
 }
 
 template <int FMT, int NSRC, int XM, int MB, int SPU, bool PERM, int CM>
@@ -920,7 +919,7 @@ int launch_t(st_context *ctx, Params &p) {
             const int cap = (int)(64ll * kChunkRounds<NSRC> * nw / ((long long)p.M * IPU * kChunkSlots));
             const int wpt = std::min(nw / tpw, cap);
             const int ch = wpt * kChunkSlots;
-            const size_t a_bytes = (size_t)ch * ((size_t)SPU * MB * 4 * p.rb * 16 + (size_t)p.M * 12);
+            const size_t a_bytes = (size_t)ch * ((size_t)SPU * MB * 4 * p.rb * 16 + (size_t)p.M * 16);
             const size_t region =
                 (a_bytes + (!is_i8(FMT) ? (size_t)tpw * p.units * NSRC * 16 : 0) + 15) & ~size_t(15);
             const size_t lds = region + (size_t)nw * NSRC * MB * 64 * sizeof(float);
@@ -1028,7 +1027,7 @@ int launch_t(st_context *ctx, Params &p) {
         return fail(ST_ERR_SHAPE, "qmv: %d groups per wave exceed the zero-point table", max_units);
     const int afr = p.chunk * SPU * MB * 4 * p.rb;
     const int ztab = (is_i8(FMT)) ? 0 : std::min(max_units, kMaxZeroUnits) * NSRC * 16;
-    p.wave_lds = (afr * 16 + p.chunk * p.M * 12 + ztab + 15) & ~15;
+    p.wave_lds = (afr * 16 + p.chunk * p.M * 16 + ztab + 15) & ~15;
     const size_t lds = (size_t)nw * p.wave_lds + (size_t)nw * NSRC * MB * 64 * sizeof(float);
     return launch_kernel<FMT, NSRC, XM, MB, SPU, PERM, 0>(ctx, p, lds);
 }
