@@ -594,3 +594,24 @@ def test_graph_replay_multi_token_split_k(gpu, orc):
         torch.cuda.synchronize()
     ref = orc.gptq_matvec_f64(cd["x"], cd["qweight"], cd["scales"], 9728, 2560, 128)
     assert orc.rel_l2(yd.cpu().numpy(), ref) < TOL
+
+
+@pytest.mark.parametrize("mode", ["1", "2"])
+@pytest.mark.parametrize("K,N,gs,Mr,zeros,act", [
+    (4096, 4096, 128, 1, False, False),   # q_proj shape, one tile per workgroup
+    (11008, 4104, 128, 1, True, True),    # long K, ragged
+    (4096, 11008, 64, 3, False, False),   # multi-tile, three tokens
+    (2560, 1024, 256, 1, True, False),
+])
+def test_staging_modes_agree(gpu, orc, mode, K, N, gs, Mr, zeros, act, monkeypatch):
+    """The single-block cooperative kernels forced into each staging mode
+    (1: staging waves, 2: every wave stages its own groups) meet the oracle's
+    bar and agree with the launcher's own choice up to f32 summation order."""
+    c = orc.gptq_case(K // 16 + N + Mr, K, N, gs, zeros=zeros, act_order=act, M=Mr)
+    w = up(gpu, c)
+    y_auto = run_matvec(gpu, w, c["x"])
+    monkeypatch.setenv("ST_QMV_STAGE_MODE", mode)
+    y = run_matvec(gpu, w, c["x"])
+    ref = orc.gptq_matvec_f64(c["x"], c["qweight"], c["scales"], K, N, gs, qzeros=c["qzeros"], g_idx=c["g_idx"])
+    assert orc.rel_l2(y, ref) < TOL
+    assert orc.rel_l2(y, y_auto) < 1e-6
