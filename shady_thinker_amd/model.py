@@ -121,6 +121,6 @@ def linear(gpu, x, w, y) -> None:
         else:
             gptq_matvec(gpu, "linear", x, w.qweight, w.scales, y, w.K, w.N, w.group_size, w.qzeros, w.perm, w.flags)
     elif isinstance(w, Int8Weight):
-        int8_matvec(gpu, x, w.w, w.scale, y, w.K, w.N)
+        int8_matvec(gpu, x, w.w, w.scale, y, w.K, w.N, w.flags)
     else:
         raise TypeError(type(w))

@@ -615,3 +615,16 @@ def test_staging_modes_agree(gpu, orc, mode, K, N, gs, Mr, zeros, act, monkeypat
     ref = orc.gptq_matvec_f64(c["x"], c["qweight"], c["scales"], K, N, gs, qzeros=c["qzeros"], g_idx=c["g_idx"])
     assert orc.rel_l2(y, ref) < TOL
     assert orc.rel_l2(y, y_auto) < 1e-6
+
+
+@pytest.mark.parametrize("tiled", [True, False])
+def test_linear_dispatch_int8_honours_layout(gpu, orc, tiled):
+    """linear() on an Int8Weight passes the weight's layout flag (tiled by
+    default at upload)."""
+    K, N, Mr = 1024, 520, 3
+    c = orc.int8_case(110, K, N, M=Mr)
+    w = sta.Int8Weight.upload(gpu, c["w"], c["scale"], tiled=tiled)
+    y = torch.empty(Mr, N, device="cuda")
+    sta.linear(gpu, torch.from_numpy(c["x"]).cuda(), w, y)
+    torch.cuda.synchronize()
+    assert orc.rel_l2(y.cpu().numpy(), orc.int8_matvec_f64(c["x"], c["w"], c["scale"], K, N)) < TOL
