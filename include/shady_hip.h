@@ -28,6 +28,11 @@
  *    keep the reference's panic semantics.
  *  - A context is not thread-safe (the reference serialises through
  *    `&mut GpuContext`).
+ *  - No call allocates. The context's workspace (st_context_reserve_workspace)
+ *    holds the prefill GEMM's pre-processed A and split-K partials, and the
+ *    split-K partials of multi-token (M > 1) decode calls on linears with few
+ *    16-column tiles; one-token decode calls use none. Calls on one context
+ *    are ordered by its stream, so they never overlap on it.
  */
 #ifndef SHADY_HIP_H
 #define SHADY_HIP_H
