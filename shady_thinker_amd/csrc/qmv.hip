@@ -86,7 +86,7 @@ constexpr int kTokenBlock = 16;
 
 template <typename F>
 int by_token_blocks(QmvParams &p, int xm, F &&launch) {
-    const int blk = std::max(1, st::qmv::env_int("ST_QMV_BLOCK", kTokenBlock));
+    const int blk = std::max(1, std::min(kTokenBlock, st::qmv::env_int("ST_QMV_BLOCK", kTokenBlock)));
     if (p.M <= blk) return launch(p);
     const size_t xe = xm == XM_F16 ? 2 : 4;
     for (int m0 = 0; m0 < p.M; m0 += blk) {

@@ -119,20 +119,14 @@ __device__ __forceinline__ float silu_f(float v) { return __fdividef(v, 1.0f + _
 // register r = J/4 holds nibbles 2(J%4) (+1 for odd r) of word r/2.
 __device__ __forceinline__ constexpr int i4_koff(int J) { return ((J >> 3) << 3) + ((J & 3) << 1) + ((J >> 2) & 1); }
 
-template <int XM>
-__device__ __forceinline__ float x_elem(const Params &p, size_t idx) {
-    if constexpr (XM == XM_F32) {
-        return static_cast<const float *>(p.x)[idx];
-    } else if constexpr (XM == XM_F16) {
-        return (float)static_cast<const _Float16 *>(p.x)[idx];
-    } else {
-        return silu_f(static_cast<const float *>(p.x)[idx]) * p.xb[idx];
-    }
-}
-
-// x[m, k .. k+15] (through perm under act-order) with 128-bit loads.
+// One staging item: x[m, k .. k+15] (through perm under act-order), loaded
+// with no arithmetic on the values, so that the loads stay in flight while
+// the wave issues its other loads (arithmetic right after a load makes the
+// wave wait for it): f32 as is; f16 as raw bits (two halves per dword, or
+// one half per dword under act-order); silu(a) * b as a in v and b in vb.
+// x_finish converts, at staging.
 template <int XM, bool PERM>
-__device__ __forceinline__ void load_x16(const Params &p, int m, int k, float v[16]) {
+__device__ __forceinline__ void load_x16(const Params &p, int m, int k, float v[16], float vb[16]) {
     const size_t row = (size_t)m * p.K;
     if constexpr (PERM) {
         int idx[16];
@@ -145,40 +139,59 @@ __device__ __forceinline__ void load_x16(const Params &p, int m, int k, float v[
             idx[4 * j + 3] = t.w;
         }
 #pragma unroll
-        for (int j = 0; j < 16; ++j) v[j] = x_elem<XM>(p, row + idx[j]);
-    } else if constexpr (XM == XM_F16) {
-        typedef _Float16 h8 __attribute__((ext_vector_type(8)));
-        const h8 *src = reinterpret_cast<const h8 *>(static_cast<const _Float16 *>(p.x) + row + k);
-        const h8 a = src[0], b = src[1];
-#pragma unroll
-        for (int j = 0; j < 8; ++j) {
-            v[j] = (float)a[j];
-            v[8 + j] = (float)b[j];
+        for (int j = 0; j < 16; ++j) {
+            if constexpr (XM == XM_F16) {
+                const unsigned short h = static_cast<const unsigned short *>(p.x)[row + idx[j]];
+                v[j] = __builtin_bit_cast(float, (unsigned)h);
+            } else {
+                v[j] = static_cast<const float *>(p.x)[row + idx[j]];
+                if constexpr (XM == XM_SILU) vb[j] = p.xb[row + idx[j]];
+            }
         }
     } else {
-        const float4 *src = reinterpret_cast<const float4 *>(static_cast<const float *>(p.x) + row + k);
-        float4 t[4];
+        // f32 / silu: 16 values; f16: 8 dwords of raw halves
+        constexpr int NV = XM == XM_F16 ? 2 : 4;
+        const float4 *src = XM == XM_F16
+                                ? reinterpret_cast<const float4 *>(static_cast<const _Float16 *>(p.x) + row + k)
+                                : reinterpret_cast<const float4 *>(static_cast<const float *>(p.x) + row + k);
 #pragma unroll
-        for (int j = 0; j < 4; ++j) t[j] = src[j];
+        for (int j = 0; j < NV; ++j) {
+            const float4 t = src[j];
+            v[4 * j] = t.x;
+            v[4 * j + 1] = t.y;
+            v[4 * j + 2] = t.z;
+            v[4 * j + 3] = t.w;
+        }
         if constexpr (XM == XM_SILU) {
             const float4 *bsrc = reinterpret_cast<const float4 *>(p.xb + row + k);
 #pragma unroll
             for (int j = 0; j < 4; ++j) {
                 const float4 u = bsrc[j];
-                v[4 * j] = silu_f(t[j].x) * u.x;
-                v[4 * j + 1] = silu_f(t[j].y) * u.y;
-                v[4 * j + 2] = silu_f(t[j].z) * u.z;
-                v[4 * j + 3] = silu_f(t[j].w) * u.w;
-            }
-        } else {
-#pragma unroll
-            for (int j = 0; j < 4; ++j) {
-                v[4 * j] = t[j].x;
-                v[4 * j + 1] = t[j].y;
-                v[4 * j + 2] = t[j].z;
-                v[4 * j + 3] = t[j].w;
+                vb[4 * j] = u.x;
+                vb[4 * j + 1] = u.y;
+                vb[4 * j + 2] = u.z;
+                vb[4 * j + 3] = u.w;
             }
         }
+    }
+}
+
+// The 16 f32 values of a staging item from what load_x16 left.
+template <int XM, bool PERM>
+__device__ __forceinline__ void x_finish(float v[16], const float vb[16]) {
+    if constexpr (XM == XM_F16) {
+        float t[16];
+#pragma unroll
+        for (int j = 0; j < 16; ++j) {
+            const unsigned d = __builtin_bit_cast(unsigned, v[PERM ? j : j / 2]);
+            const unsigned short h = (unsigned short)(PERM ? d : ((j & 1) ? d >> 16 : d & 0xFFFFu));
+            t[j] = (float)__builtin_bit_cast(_Float16, h);
+        }
+#pragma unroll
+        for (int j = 0; j < 16; ++j) v[j] = t[j];
+    } else if constexpr (XM == XM_SILU) {
+#pragma unroll
+        for (int j = 0; j < 16; ++j) v[j] = silu_f(v[j]) * vb[j];
     }
 }
 
@@ -234,6 +247,9 @@ constexpr int kMaxTilesPerWg = 4;  // COOP: tiles one workgroup may own
 constexpr int kRingBeforeBarrier = 2;
 
 constexpr int kCoopRounds = 4;  // x staging rounds per staging wave in COOP kernels
+// (silu(a) * b holds a and b until staging: two rounds, within the registers)
+template <int XM>
+constexpr int coop_rounds = XM == XM_SILU ? 2 : kCoopRounds;
 // CHK kernels: consecutive groups per wave per K chunk (the ring depth); 3
 // and 4 measured slower (32 INT8 tokens: 84 and 119 against 65 us)
 constexpr int kChunkSlots = 2;
@@ -279,7 +295,7 @@ __global__ __launch_bounds__((64 * (CM == 3 ? kChunkWaves<NSRC, MB> : kMaxWavesF
     constexpr int IPU = 4 * SPU;                              // 16-k items per group and token
     constexpr int WPU = (is_i8(FMT)) ? 4 * SPU : 2 * SPU;  // weight dwords per lane per group
     // staging rounds per lane: per-wave chunk (fallback) or whole slice (COOP)
-    constexpr int RMAX = CHK ? kChunkRounds<NSRC> : (COOP ? kCoopRounds : (4 * MB * IPU + 63) / 64);
+    constexpr int RMAX = CHK ? kChunkRounds<NSRC> : (COOP ? coop_rounds<XM> : (4 * MB * IPU + 63) / 64);
 
     constexpr bool SCB = (CM == 1 || CM == 2) && !is_i8(FMT);  // per-wave scale block (see below)
     const int tid = threadIdx.x;
@@ -453,6 +469,7 @@ __global__ __launch_bounds__((64 * (CM == 3 ? kChunkWaves<NSRC, MB> : kMaxWavesF
     const int wave0 = (COOP && !PW) ? wave : 0;  // row of round 0
     int uend = (COOP && !PW) ? p.units : u1;  // staged groups end here (CHK: per chunk)
     float xv[RMAX][16];
+    float xb[XM == XM_SILU ? RMAX : 1][16];  // silu(a) * b: b
     // A wave with no item in a round skips it (loads and work): the branch
     // is uniform per wave and the same condition guards the loads and their
     // only consumer, stage().
@@ -468,7 +485,7 @@ __global__ __launch_bounds__((64 * (CM == 3 ? kChunkWaves<NSRC, MB> : kMaxWavesF
                 w = i - m * (SW * IPU);
             }
             const int u = min(cs + w / IPU, uend - 1);
-            load_x16<XM, PERM>(p, m, u * p.gs + 16 * (w % IPU), xv[r]);
+            load_x16<XM, PERM>(p, m, u * p.gs + 16 * (w % IPU), xv[r], xb[XM == XM_SILU ? r : 0]);
         }
     };
     auto stage = [&](int cs) {
@@ -485,6 +502,7 @@ __global__ __launch_bounds__((64 * (CM == 3 ? kChunkWaves<NSRC, MB> : kMaxWavesF
             const int ui = w / IPU, ii = w % IPU;
             const int ua = (COOP && !CHK) ? cs + ui : ui;  // A-region unit (COOP: the group itself)
             const bool ok = i < items && cs + ui < uend;
+            x_finish<XM, PERM>(xv[r], xb[XM == XM_SILU ? r : 0]);
             float amax = 0.0f, nf = 0.0f;
 #pragma unroll
             for (int j = 0; j < 16; ++j) {
@@ -848,7 +866,8 @@ inline int env_int(const char *name, int dflt) {
     return (v && *v) ? std::atoi(v) : dflt;
 }
 
-inline int mb_for(int M) { return M <= 4 ? 1 : (M <= 8 ? 2 : (M <= 16 ? 4 : 8)); }
+// MFMA token blocks of 4 per launch (calls run in blocks of at most 16 tokens)
+inline int mb_for(int M) { return M <= 4 ? 1 : (M <= 8 ? 2 : 4); }
 
 // Bytes of one staged group (A operands, scalars, zero table row).
 template <int FMT, int NSRC, int MB, int SPU>
@@ -948,7 +967,7 @@ int launch_t(st_context *ctx, Params &p) {
         const long long items = (long long)p.M * p.units * IPU;
         // launches the COOP kernel with this shape if it fits; -1 = it does not.
         // Staging waves: as many as one round each needs (staging latency),
-        // fewer (up to kCoopRounds rounds each) when K needs the waves.
+        // fewer (up to coop_rounds rounds each) when K needs the waves.
         auto try_coop = [&](int nw, int tpw, int grid) -> int {
             const size_t ub = unit_bytes<FMT, NSRC, MB, SPU>(p);
             const size_t region =
@@ -967,11 +986,12 @@ int launch_t(st_context *ctx, Params &p) {
             // stream weights. ST_QMV_STAGE_MODE / _ROUNDS override (tuning).
             const int mode = env_int("ST_QMV_STAGE_MODE", 0);
             const int env_r = env_int("ST_QMV_STAGE_ROUNDS", 0);
-            const int r0 = env_r > 0 ? std::min(env_r, kCoopRounds) : (tpw > 1 ? 2 : 1);
+            constexpr int CR = coop_rounds<XM>;
+            const int r0 = env_r > 0 ? std::min(env_r, CR) : std::min(CR, tpw > 1 ? 2 : 1);
             const long long ns0 = (items + 64 * r0 - 1) / (64 * r0);
             const bool per_wave = mode == 2 || (mode == 0 && (ns0 >= 6 || XM == XM_SILU));
             if (!per_wave) {
-                for (int rounds = r0; rounds <= kCoopRounds; ++rounds) {
+                for (int rounds = r0; rounds <= CR; ++rounds) {
                     const long long ns = (items + 64 * rounds - 1) / (64 * rounds);
                     const long long wpt = (nw - ns) / tpw;  // compute waves per tile in the fullest workgroup
                     if (wpt < 1) continue;
@@ -985,7 +1005,7 @@ int launch_t(st_context *ctx, Params &p) {
             if (wpt < 1) return -1;
             const int upw = (p.units + wpt - 1) / wpt;  // groups per wave
             if (!is_i8(FMT) && upw > kScaleUnits) return -1;
-            if ((long long)p.M * upw * IPU > 64ll * kCoopRounds) return -1;  // its staging rounds
+            if ((long long)p.M * upw * IPU > 64ll * CR) return -1;  // its staging rounds
             p.nstage = 0;
             return launch_kernel<FMT, NSRC, XM, MB, SPU, PERM, 2>(ctx, p, lds);
         };
@@ -1037,10 +1057,11 @@ int launch_mb(st_context *ctx, Params &p) {
     switch (mb_for(p.M)) {
         case 1: return launch_t<FMT, NSRC, XM, 1, SPU, PERM>(ctx, p);
         case 2: return launch_t<FMT, NSRC, XM, 2, SPU, PERM>(ctx, p);
-        case 4: return launch_t<FMT, NSRC, XM, 4, SPU, PERM>(ctx, p);
+        case 4:
+            if (p.M <= 16) return launch_t<FMT, NSRC, XM, 4, SPU, PERM>(ctx, p);
+            [[fallthrough]];
         default:
-            if constexpr (NSRC == 1) return launch_t<FMT, NSRC, XM, 8, SPU, PERM>(ctx, p);
-            return fail(ST_ERR_SHAPE, "qmv: M too large for the dual kernel");
+            return fail(ST_ERR_SHAPE, "qmv: %d tokens in one launch (at most 16)", p.M);
     }
 }
 
