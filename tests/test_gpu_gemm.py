@@ -197,3 +197,12 @@ def test_gemm_tile_widths_agree(gpu, orc, Mr, K, N, gs, zeros, act, monkeypatch)
     ref = orc.gptq_matvec_f64(c["x"], c["qweight"], c["scales"], K, N, gs, qzeros=c["qzeros"], g_idx=c["g_idx"])
     assert np.array_equal(ys["1"], ys["2"])
     assert orc.rel_l2(ys["1"], ref) < 5e-4
+
+
+def test_gemm_long_k(gpu, orc):
+    Mr, K, N, gs = 80, 32768, 264, 128
+    c = orc.gptq_case(120, K, N, gs, zeros=True, act_order=True, M=Mr, x_dtype=np.float16)
+    w = up(gpu, c)
+    y = run_gemm(gpu, w, c["x"])
+    ref = orc.gptq_matvec_f64(c["x"], c["qweight"], c["scales"], K, N, gs, qzeros=c["qzeros"], g_idx=c["g_idx"])
+    assert orc.rel_l2(y, ref) < 5e-4

@@ -628,3 +628,15 @@ def test_linear_dispatch_int8_honours_layout(gpu, orc, tiled):
     sta.linear(gpu, torch.from_numpy(c["x"]).cuda(), w, y)
     torch.cuda.synchronize()
     assert orc.rel_l2(y.cpu().numpy(), orc.int8_matvec_f64(c["x"], c["w"], c["scale"], K, N)) < TOL
+
+
+@pytest.mark.parametrize("K,gs,Mr", [(32768, 128, 1), (16384, 64, 5), (24576, 256, 1)])
+def test_long_k(gpu, orc, K, gs, Mr):
+    """K at the largest sizes the entry points take (up to 32768): the
+    launcher's path for long K (LDS limits the cooperative staging)."""
+    N = 264
+    c = orc.gptq_case(K // 1024 + Mr, K, N, gs, zeros=True, act_order=True, M=Mr)
+    w = up(gpu, c)
+    y = run_matvec(gpu, w, c["x"])
+    ref = orc.gptq_matvec_f64(c["x"], c["qweight"], c["scales"], K, N, gs, qzeros=c["qzeros"], g_idx=c["g_idx"])
+    assert orc.rel_l2(y, ref) < TOL
