@@ -58,4 +58,8 @@ inline int launch_check(const char *what) {
     return ST_OK;
 }
 
+// Multi-token INT8 matvec with f16 x on f16 MFMA (i8mm.hip); the caller
+// (st_int8_matvec) has checked the arguments.
+int int8_mm_f16(st_context *ctx, const void *x, const int8_t *w, const float *scale, float *y, int M, int K, int N);
+
 }  // namespace st

@@ -84,6 +84,9 @@ int launch_i4(st_context *ctx, QmvParams &p, bool tiled, int nsrc, int xm) {
 // design for M > 4.)
 constexpr int kTokenBlock = 16;
 
+// Fewest tokens for which st_int8_matvec takes the f16-MFMA kernel (f16 x, tiled weights).
+constexpr int kI8mmMinM = 2;
+
 template <typename F>
 int by_token_blocks(QmvParams &p, int xm, F &&launch) {
     const int blk = std::max(1, std::min(kTokenBlock, st::qmv::env_int("ST_QMV_BLOCK", kTokenBlock)));
@@ -246,6 +249,10 @@ int st_int8_matvec(st_context *ctx, const void *x, int x_dtype, const int8_t *w,
     if (!st::aligned16(w) || !st::aligned16(x))
         return st::fail(ST_ERR_ALIGN, "st_int8_matvec: w and x must be 16-byte aligned");
     if (x_dtype != ST_F32 && x_dtype != ST_F16) return st::fail(ST_ERR_INVALID, "st_int8_matvec: x_dtype %d", x_dtype);
+    // Several tokens with f16 x on tiled weights: the f16-MFMA skinny GEMM,
+    // which reads the weights once for all tokens.
+    if (tiled && x_dtype == ST_F16 && M >= st::qmv::env_int("ST_I8MM_MIN_M", kI8mmMinM))
+        return st::int8_mm_f16(ctx, x, w, scale, y, M, K, N);
     QmvParams p{};
     p.x = x;
     p.w8 = w;

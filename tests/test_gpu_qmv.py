@@ -481,9 +481,12 @@ def test_int8_repack_layout(gpu, orc):
 
 
 @pytest.mark.parametrize("Mr", [1, 3, 8, 16, 32])
-def test_int8_tiled_equals_row_major(gpu, orc, Mr):
-    """Tiled and row-major INT8 weights give the same y bit for bit (the same
-    integer products in the same order), within the bar of the f64 oracle."""
+def test_int8_tiled_equals_row_major(gpu, orc, Mr, monkeypatch):
+    """Tiled and row-major INT8 weights give the same y bit for bit through
+    the integer-limb kernels (the same integer products in the same order),
+    within the bar of the f64 oracle. (Several f16 tokens on tiled weights
+    normally take the f16-MFMA kernel; it is switched off here.)"""
+    monkeypatch.setenv("ST_I8MM_MIN_M", "99")
     K, N = 5120, 4104
     c = orc.int8_case(84 + Mr, K, N, M=Mr)
     x = torch.from_numpy(c["x"]).cuda()
@@ -640,3 +643,75 @@ def test_long_k(gpu, orc, K, gs, Mr):
     y = run_matvec(gpu, w, c["x"])
     ref = orc.gptq_matvec_f64(c["x"], c["qweight"], c["scales"], K, N, gs, qzeros=c["qzeros"], g_idx=c["g_idx"])
     assert orc.rel_l2(y, ref) < TOL
+
+
+@pytest.mark.parametrize("Mr,K,N", [
+    (2, 128, 20),       # one group, one partial chunk, two tiles
+    (5, 384, 36),       # ragged N, partial chunk
+    (16, 1152, 264),    # one 16-row block, a chunk and a bit
+    (17, 5120, 1000),   # two row blocks, 63 tiles (one per workgroup)
+    (32, 2176, 4104),   # 257 tiles: one or two per workgroup
+    (8, 256, 24576),    # 1536 tiles: six per workgroup, two waves per tile
+    (3, 256, 36880),    # 2305 tiles: more than eight per CU, more workgroups than CUs
+])
+def test_int8_mm_f16(gpu, orc, Mr, K, N, monkeypatch):
+    """Several f16 tokens on tiled INT8 weights: the f16-MFMA kernel (every
+    int8 weight and f16 x exact in f16, products exact in f32, f32 sums)
+    against the f64 oracle, and against the integer-limb kernels."""
+    c = orc.int8_case(120 + Mr, K, N, M=Mr)
+    w = sta.Int8Weight.upload(gpu, c["w"], c["scale"])
+    x = torch.from_numpy(c["x"]).cuda()
+
+    def run():
+        y = torch.full((Mr, N), float("nan"), device="cuda")
+        M.int8_matvec(gpu, x, w.w, w.scale, y, K, N, w.flags)
+        torch.cuda.synchronize()
+        return y.cpu().numpy()
+
+    y = run()
+    ref = orc.int8_matvec_f64(c["x"], c["w"], c["scale"], K, N)
+    e = orc.rel_l2(y, ref)
+    print(f"int8 f16-MFMA M={Mr} K={K} N={N} rel-L2 {e:.3e}")
+    assert np.isfinite(y).all() and e < 1e-6  # f32 summation error only
+    monkeypatch.setenv("ST_I8MM_MIN_M", "99")
+    assert orc.rel_l2(run(), ref) < TOL
+
+
+def test_int8_mm_f16_integer_exact(gpu, orc):
+    """Integer x (|x| <= 4) and unit scales: every partial sum is an integer
+    below 2^24, so the f16-MFMA kernel's y equals the exact integer product
+    bit for bit."""
+    Mr, K, N = 32, 3072, 520
+    rng = np.random.default_rng(7)
+    wq = rng.integers(-127, 128, size=(N, K), dtype=np.int8)
+    xi = rng.integers(-4, 5, size=(Mr, K)).astype(np.float16)
+    w = sta.Int8Weight.upload(gpu, wq, np.ones(N, np.float32))
+    y = torch.empty(Mr, N, device="cuda")
+    M.int8_matvec(gpu, torch.from_numpy(xi).cuda(), w.w, w.scale, y, K, N, w.flags)
+    torch.cuda.synchronize()
+    exact = xi.astype(np.int64) @ wq.astype(np.int64).T
+    assert np.array_equal(y.cpu().numpy(), exact.astype(np.float32))
+
+
+def test_int8_mm_f16_graph_replay(gpu, orc):
+    """The f16-MFMA kernel under graph capture: every replay equals the eager
+    result bit for bit (no workspace, no memset)."""
+    Mr, K, N = 24, 1280, 1040
+    c = orc.int8_case(140, K, N, M=Mr)
+    w = sta.Int8Weight.upload(gpu, c["w"], c["scale"])
+    x = torch.from_numpy(c["x"]).cuda()
+    y = torch.empty(Mr, N, device="cuda")
+    M.int8_matvec(gpu, x, w.w, w.scale, y, K, N, w.flags)
+    torch.cuda.synchronize()
+    eager = y.clone()
+    s = torch.cuda.Stream()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.stream(s):
+        with torch.cuda.graph(g, stream=s):
+            M.int8_matvec(gpu, x, w.w, w.scale, y, K, N, w.flags)
+    for _ in range(3):
+        y.zero_()
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(y, eager)
