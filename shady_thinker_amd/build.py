@@ -18,7 +18,7 @@ OBJ = os.path.join(HERE, "_build")
 LIB = os.path.join(HERE, "libshady_hip.so")
 SOURCES = [
     "runtime.hip", "qmv.hip", "qmv_i4_p0.hip", "qmv_i4_p1.hip", "qmv_i4t_p0.hip", "qmv_i4t_p1.hip", "qmv_i8.hip", "qmv_i8t.hip",
-    "i8mm.hip", "dequant.hip", "gemm.hip", "bf16mv.hip",
+    "i8mm.hip", "i4mm.hip", "dequant.hip", "gemm.hip", "bf16mv.hip",
 ]
 
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")

@@ -1,0 +1,452 @@
+// Multi-token GPTQ int4 decode on f16 MFMA (a skinny GEMM), for 2..16
+// tokens on tiled weights (st_gptq_i4_repack) without act-order:
+//   y[m, n]  = sum_g s[g, n] * sum_{k in g} (q[k, n] - z[g, n]) * x[m, k]
+//   (st_gptq_i4_matvec), or silu(gate) * up of two such sums
+//   (st_gptq_i4_gate_up_silu). Semantics of gptq_matvec.wgsl:51-58 and
+//   fused_gate_up_silu_4t.wgsl:24-90; the reference runs one token at a time.
+//
+//  * Exact products: (q - z) is an integer in [-15, 15], exact in f16 (the
+//    f16 1024 bias: 1024 + q, minus 1024 + z). f16 x is used as is. f32 x is
+//    split once, by a pre-pass into the context workspace, per token and per
+//    128 k: x 2^-e (2^e just above the block's largest |x|) = hi + lo, two
+//    f16 rows of the MFMA A operand (about 22 significant bits). Every product is exact in f32; each 64 (or 128) k
+//    block sums into a fresh accumulator that is then scaled by s 2^e in f32.
+//  * Every weight is read from HBM once for all tokens (the integer-limb
+//    matvec kernels grow their per-token staging and epilogue work with M).
+//  * Work split as in i8mm.hip: one workgroup per CU owns a run of 16-column
+//    tiles (gate/up: the gate and up tiles of each); S waves per tile each
+//    take one 128-k unit of every S-unit chunk. x is copied per chunk into
+//    LDS (double buffered, one chunk ahead); each wave keeps a ring of three
+//    chunks of weights, scales and zeros, two in flight while it computes
+//    one. Partial sums meet in LDS in a fixed order.
+#include "common.hpp"
+
+#include <algorithm>
+#include <cstdlib>
+#include <type_traits>
+
+namespace {
+
+typedef _Float16 half8 __attribute__((ext_vector_type(8)));
+typedef _Float16 half2_t __attribute__((ext_vector_type(2)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x2 __attribute__((ext_vector_type(2)));
+typedef unsigned u32x4 __attribute__((ext_vector_type(4)));
+typedef unsigned u32x2 __attribute__((ext_vector_type(2)));
+
+constexpr int kWaves = 16;
+constexpr int kThreads = 64 * kWaves;
+constexpr int kTileN = 16;
+constexpr int kRsrcWord3 = 0x00020000;     // raw 32-bit buffer data (gfx9-class)
+constexpr unsigned kNoLoad = 0x80000000u;  // buffer offset past every resource: reads 0, touches no memory
+constexpr int kMaxTilesPerWg = 8;
+
+// v_and_or_b32 with both constants in registers (a VOP3 takes no literal).
+__device__ __forceinline__ unsigned and_or(unsigned a, unsigned m, unsigned c) {
+    unsigned r;
+    asm("v_and_or_b32 %0, %1, %2, %3" : "=v"(r) : "v"(a), "v"(m), "v"(c));
+    return r;
+}
+
+// GPTQ word (nibbles n0..n7 = k0..k7) -> (n0 - z, n4 - z), (n1 - z, n5 - z),
+// (n2 - z, n6 - z), (n3 - z, n7 - z) in f16, exactly: 1024 + n - (1024 + z),
+// or (1024 + 16 n) / 16 - (64 + z) for the odd nibbles.
+__device__ __forceinline__ half8 word_to_b(unsigned w, half2_t zlo, half2_t zhi) {
+    const unsigned m_lo = 0x000F000Fu, m_hi = 0x00F000F0u, bias = 0x64006400u;
+    const half2_t sixteenth = {(_Float16)0.0625f, (_Float16)0.0625f};
+    const unsigned w8 = w >> 8;
+    const half2_t h0 = __builtin_bit_cast(half2_t, and_or(w, m_lo, bias)) - zlo;
+    const half2_t h1 = __builtin_elementwise_fma(__builtin_bit_cast(half2_t, and_or(w, m_hi, bias)), sixteenth, zhi);
+    const half2_t h2 = __builtin_bit_cast(half2_t, and_or(w8, m_lo, bias)) - zlo;
+    const half2_t h3 = __builtin_elementwise_fma(__builtin_bit_cast(half2_t, and_or(w8, m_hi, bias)), sixteenth, zhi);
+    const u32x4 r = {__builtin_bit_cast(unsigned, h0), __builtin_bit_cast(unsigned, h1), __builtin_bit_cast(unsigned, h2),
+                     __builtin_bit_cast(unsigned, h3)};
+    return __builtin_bit_cast(half8, r);
+}
+
+// 8 halves (k0..k7, as 4 dwords) -> the order of word_to_b: k0,k4,k1,k5,k2,k6,k3,k7.
+__device__ __forceinline__ u32x4 to_b_order(u32x4 a) {
+    u32x4 r;
+    r.x = __builtin_amdgcn_perm(a.z, a.x, 0x05040100u);
+    r.y = __builtin_amdgcn_perm(a.z, a.x, 0x07060302u);
+    r.z = __builtin_amdgcn_perm(a.w, a.y, 0x05040100u);
+    r.w = __builtin_amdgcn_perm(a.w, a.y, 0x07060302u);
+    return r;
+}
+
+template <int CTRL>
+__device__ __forceinline__ float dpp_f(float v) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), CTRL, 0xF, 0xF, true));
+}
+// max over the 16 lanes of a DPP row
+__device__ __forceinline__ float row_max(float v) {
+    v = fmaxf(v, dpp_f<0xB1>(v));   // quad_perm [1,0,3,2]
+    v = fmaxf(v, dpp_f<0x4E>(v));   // quad_perm [2,3,0,1]
+    v = fmaxf(v, dpp_f<0x141>(v));  // row_half_mirror
+    v = fmaxf(v, dpp_f<0x140>(v));  // row_mirror
+    return v;
+}
+
+// silu(v) = v / (1 + exp(-v)) (fused_gate_up_silu_4t.wgsl)
+__device__ __forceinline__ float silu_f(float v) { return __fdividef(v, 1.0f + __expf(-v)); }
+
+__device__ __forceinline__ void lds_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
+
+template <int GS>
+struct Unit {  // what a wave loads for one 128-k unit of its tile and source
+    static constexpr int NG = GS == 64 ? 2 : 1;  // groups in the unit
+    u32x4 w;                                      // words (st, h) = (0,0), (0,1), (1,0), (1,1)
+    unsigned s[NG];                               // raw f16 scale (low half)
+    unsigned z[NG];                               // raw qzeros word
+};
+
+// f32 x -> rows 2t (hi) and 2t + 1 (lo) of xp [2M, K] f16 and the factor
+// 2^e of each (token, 128-k unit) in pe [M, K / 128]: x 2^-e = hi + lo with
+// |x 2^-e| < 1 over the unit. Every 8 k are stored in the B order of
+// word_to_b. One 16-lane DPP row per (token, unit), 8 k per lane.
+__global__ __launch_bounds__(256) void i4mm_prep_kernel(const float *__restrict__ x, _Float16 *__restrict__ xp,
+                                                        float *__restrict__ pe, int M, int K) {
+    const int units = K / 128;
+    const int gid = blockIdx.x * 16 + (threadIdx.x >> 4), l = threadIdx.x & 15;
+    const bool ok = gid < M * units;  // every lane runs the DPP max below
+    const int t = ok ? gid / units : 0, u = ok ? gid % units : 0;
+    const size_t k = (size_t)u * 128 + 8 * l;
+    f32x4 a = {0.f, 0.f, 0.f, 0.f}, b = a;
+    if (ok) {
+        a = *reinterpret_cast<const f32x4 *>(x + (size_t)t * K + k);
+        b = *reinterpret_cast<const f32x4 *>(x + (size_t)t * K + k + 4);
+    }
+    const float v[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+    float amax = 0.f;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) amax = fmaxf(amax, fabsf(v[e]));
+    amax = row_max(amax);
+    const int ex = amax > 0.f ? __builtin_amdgcn_frexp_expf(amax) : 0;  // amax < 2^ex
+    const float down = __builtin_amdgcn_ldexpf(1.0f, -ex);
+    _Float16 hi[8], lo[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+        const float xv = v[e] * down;
+        hi[e] = (_Float16)xv;
+        lo[e] = (_Float16)(xv - (float)hi[e]);
+    }
+    u32x4 H, L;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+        H[e] = (unsigned)__builtin_bit_cast(uint16_t, hi[2 * e]) | ((unsigned)__builtin_bit_cast(uint16_t, hi[2 * e + 1]) << 16);
+        L[e] = (unsigned)__builtin_bit_cast(uint16_t, lo[2 * e]) | ((unsigned)__builtin_bit_cast(uint16_t, lo[2 * e + 1]) << 16);
+    }
+    if (!ok) return;
+    *reinterpret_cast<u32x4 *>(xp + (size_t)(2 * t) * K + k) = to_b_order(H);
+    *reinterpret_cast<u32x4 *>(xp + (size_t)(2 * t + 1) * K + k) = to_b_order(L);
+    if (l == 0) pe[(size_t)t * units + u] = __builtin_amdgcn_ldexpf(1.0f, ex);
+}
+
+// F32X: x is the pre-pass output (xp, pe: two f16 rows per token) or f16 x;
+// NSRC: 1 (matvec) or 2 (gate/up); MB: 16-row MFMA blocks; KCU: 128-k units
+// per staged chunk; GW: units per wave per chunk (S = KCU / GW waves per tile
+// and source).
+template <bool F32X, int NSRC, int MB, int GS, int KCU, int GW>
+__global__ __launch_bounds__(kThreads) void i4mm_kernel(const void *__restrict__ x, const float *__restrict__ pe,
+                                                        const uint32_t *__restrict__ qw0,
+                                                        const uint16_t *__restrict__ sc0, const uint32_t *__restrict__ qz0,
+                                                        const uint32_t *__restrict__ qw1, const uint16_t *__restrict__ sc1,
+                                                        const uint32_t *__restrict__ qz1, int zoff, float *__restrict__ y,
+                                                        int M, int K, int N, int ntiles) {
+    constexpr int kKC = 128 * KCU;        // k per staged chunk
+    constexpr int kPitch = kKC + 8;       // halves per LDS row (16-byte pad: fragment rows on distinct banks)
+    constexpr int S = KCU / GW;
+    constexpr int R = F32X ? 2 : 1;       // MFMA rows per token
+    constexpr int ROWS = 16 * MB;
+    constexpr int TPB = 16 / R;           // tokens per 16-row block
+    constexpr int NG = Unit<GS>::NG;
+    constexpr int EK = GS == 64 ? 2 : 4;  // MFMA steps (32 k) per scaled block
+    // x items of 8 k: rows (tokens, or hi/lo rows of f32 tokens) x kKC / 8
+    // per chunk, one 16-byte load each
+    constexpr int XITEMS = ROWS * (kKC / 8);
+    constexpr int XL = (XITEMS + kThreads - 1) / kThreads;
+    // two x buffers; at the end, the partial sums of every wave
+    constexpr int kRedBytes = kWaves * MB * (F32X ? 2 : 4) * 64 * 4;
+    constexpr int kXsHalves = 2 * ROWS * kPitch > kRedBytes / 2 ? 2 * ROWS * kPitch : kRedBytes / 2;
+    __shared__ __align__(16) _Float16 xs[kXsHalves];
+    _Float16 *const xs0 = xs, *const xs1 = xs + ROWS * kPitch;
+    __shared__ float ps0[F32X ? KCU * 16 : 1];  // 2^e per (unit, token) of the chunk in xs0 / xs1
+    __shared__ float ps1[F32X ? KCU * 16 : 1];
+
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int t0 = (int)((long long)blockIdx.x * ntiles / gridDim.x);
+    const int t1 = (int)((long long)(blockIdx.x + 1) * ntiles / gridDim.x);
+    const int tb = wave / (NSRC * S), src = (wave / S) % NSRC, slice = wave % S;
+    const bool active = t0 + tb < t1;
+    const int T = min(t0 + tb, ntiles - 1);
+    const int G = K / GS;
+    const int units = K / 128;
+    const int nch = (units + KCU - 1) / KCU;
+    const int q = lane >> 4, r16 = lane & 15;
+    const int n = min(kTileN * T + r16, N - 1);  // this lane's column (the last tile's padding repeats N - 1)
+
+    const uint32_t *qw = (NSRC == 2 && src) ? qw1 : qw0;
+    const uint16_t *sc = (NSRC == 2 && src) ? sc1 : sc0;
+    const uint32_t *qz = (NSRC == 2 && src) ? qz1 : qz0;
+    const bool has_z = qz != nullptr;
+    const __amdgpu_buffer_rsrc_t rx = __builtin_amdgcn_make_buffer_rsrc((void *)x, (short)0, 0x7FFFFFFF, kRsrcWord3);
+    const __amdgpu_buffer_rsrc_t rw = __builtin_amdgcn_make_buffer_rsrc((void *)qw, (short)0, 0x7FFFFFFF, kRsrcWord3);
+    const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc((void *)sc, (short)0, 0x7FFFFFFF, kRsrcWord3);
+    const __amdgpu_buffer_rsrc_t rp = __builtin_amdgcn_make_buffer_rsrc((void *)pe, (short)0, 0x7FFFFFFF, kRsrcWord3);
+    // without qzeros the zero loads read nothing (z = 8)
+    const __amdgpu_buffer_rsrc_t rz =
+        __builtin_amdgcn_make_buffer_rsrc((void *)(has_z ? (const void *)qz : (const void *)sc), (short)0, 0x7FFFFFFF,
+                                          kRsrcWord3);
+
+    // ------------------------------------------------------------- x staging
+    // Rows already in B order: the chunk is copied. With f32 x, threads
+    // tid < KCU 16 also copy the chunk's 2^e factors (unit tid / 16, token tid % 16).
+    const int nrows = F32X ? 2 * M : M;
+    u32x4 xr2[1][XL];  // the next chunk of x
+    unsigned pr2[1];
+    auto load_x = [&](u32x4 (&xr)[XL], unsigned &pr, int c) {
+#pragma unroll
+        for (int j = 0; j < XL; ++j) {
+            const int i = j * kThreads + tid;
+            const int row = i / (kKC / 8), k = c * kKC + 8 * (i % (kKC / 8));
+            const bool ok = i < XITEMS && row < nrows && k < K;
+            xr[j] = __builtin_amdgcn_raw_buffer_load_b128(rx, ok ? (unsigned)(row * K + k) * 2u : kNoLoad, 0, 0);
+        }
+        if constexpr (F32X) {
+            const int t = tid & 15, u = c * KCU + (tid >> 4);
+            const bool ok = tid < KCU * 16 && t < M && u < units;
+            pr = __builtin_amdgcn_raw_buffer_load_b32(rp, ok ? (unsigned)(t * units + u) * 4u : kNoLoad, 0, 0);
+        }
+    };
+    auto store_x = [&](const u32x4 (&xr)[XL], unsigned pr, _Float16 *xs, float *ps) {
+#pragma unroll
+        for (int j = 0; j < XL; ++j) {
+            const int i = j * kThreads + tid;
+            if (XITEMS % kThreads == 0 || i < XITEMS)
+                *reinterpret_cast<u32x4 *>(&xs[(i / (kKC / 8)) * kPitch + 8 * (i % (kKC / 8))]) =
+                    F32X ? xr[j] : to_b_order(xr[j]);
+        }
+        if constexpr (F32X) {
+            if (tid < KCU * 16) ps[tid] = __builtin_bit_cast(float, pr);
+        }
+    };
+
+    // ------------------------------------------------------ weights, scales
+    // Tiled words of group g: lane l's GS / 32 words at ((T G + g) 64 + l) GS / 32,
+    // word 2 st + h = packed row GS / 8 g + 8 st + 2 (l / 16) + h.
+    Unit<GS> ur[3][GW];  // a ring of three chunks: loaded two chunks ahead
+    auto load_u = [&](Unit<GS> (&dst)[GW], int c) {
+#pragma unroll
+        for (int gi = 0; gi < GW; ++gi) {
+            const int u = c * KCU + slice * GW + gi;
+            const bool ok = active && u < units;
+            if constexpr (GS == 64) {
+                const unsigned o0 = ok ? (unsigned)(((T * G + 2 * u) * 64 + lane) * 8) : kNoLoad;
+                const u32x2 a = __builtin_amdgcn_raw_buffer_load_b64(rw, o0, 0, 0);
+                const u32x2 b = __builtin_amdgcn_raw_buffer_load_b64(rw, o0, 64 * 8, 0);
+                dst[gi].w = u32x4{a.x, a.y, b.x, b.y};
+            } else if constexpr (GS == 128) {
+                dst[gi].w = __builtin_amdgcn_raw_buffer_load_b128(
+                    rw, ok ? (unsigned)(((T * G + u) * 64 + lane) * 16) : kNoLoad, 0, 0);
+            } else {
+                dst[gi].w = __builtin_amdgcn_raw_buffer_load_b128(
+                    rw, ok ? (unsigned)(((T * G + u / 2) * 64 + lane) * 32 + 16 * (u & 1)) : kNoLoad, 0, 0);
+            }
+#pragma unroll
+            for (int j = 0; j < NG; ++j) {
+                const int g = GS == 64 ? 2 * u + j : (u * 128) / GS;
+                dst[gi].s[j] = __builtin_amdgcn_raw_buffer_load_b16(rs, ok ? (unsigned)(g * N + n) * 2u : kNoLoad, 0, 0);
+                dst[gi].z[j] = __builtin_amdgcn_raw_buffer_load_b32(
+                    rz, (ok && has_z) ? (unsigned)(g * (N / 8) + n / 8) * 4u : kNoLoad, 0, 0);
+            }
+        }
+    };
+
+    // Running sums: F32X: tokens TPB mb + 2 q + t2 (t2 < 2); f16: rows 16 mb + 4 q + i.
+    constexpr int YV = F32X ? 2 : 4;
+    float ys[MB][YV];
+#pragma unroll
+    for (int mb = 0; mb < MB; ++mb)
+#pragma unroll
+        for (int i = 0; i < YV; ++i) ys[mb][i] = 0.f;
+
+    auto compute = [&](const _Float16 *xs, const float *ps, const Unit<GS> (&src_u)[GW]) {
+#pragma unroll
+        for (int gi = 0; gi < GW; ++gi) {
+            const int ul = slice * GW + gi;  // unit within the chunk
+            f32x2 pw[MB];                     // 2^e of this lane's two tokens per block
+            if constexpr (F32X) {
+#pragma unroll
+                for (int mb = 0; mb < MB; ++mb) pw[mb] = *reinterpret_cast<const f32x2 *>(&ps[ul * 16 + TPB * mb + 2 * q]);
+            }
+#pragma unroll
+            for (int blk = 0; blk < 4 / EK; ++blk) {  // scaled blocks of EK steps
+                const int j = GS == 64 ? blk : 0;      // group of the block within the unit
+                const int z = has_z ? (int)((src_u[gi].z[j] >> (4 * (n & 7))) & 0xF) + zoff : 8;
+                const _Float16 zl = (_Float16)(1024 + z), zh = (_Float16)(-(64 + z));
+                const half2_t zlo = {zl, zl}, zhi = {zh, zh};
+                const float s = (float)__builtin_bit_cast(_Float16, (uint16_t)src_u[gi].s[j]);
+                f32x4 acc[MB];
+#pragma unroll
+                for (int mb = 0; mb < MB; ++mb) acc[mb] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+                for (int e = 0; e < EK; ++e) {
+                    const int step = blk * EK + e;  // word 2 st + h
+                    const int st = step >> 1, h = step & 1;
+                    const half8 b = word_to_b(src_u[gi].w[step], zlo, zhi);
+                    const int kk = ul * 128 + 64 * st + 16 * q + 8 * h;
+#pragma unroll
+                    for (int mb = 0; mb < MB; ++mb) {
+                        const half8 a = *reinterpret_cast<const half8 *>(&xs[(16 * mb + r16) * kPitch + kk]);
+                        acc[mb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, acc[mb], 0, 0, 0);
+                    }
+                }
+#pragma unroll
+                for (int mb = 0; mb < MB; ++mb) {
+                    if constexpr (F32X) {
+                        ys[mb][0] = __builtin_fmaf(s * pw[mb].x, acc[mb][0] + acc[mb][1], ys[mb][0]);
+                        ys[mb][1] = __builtin_fmaf(s * pw[mb].y, acc[mb][2] + acc[mb][3], ys[mb][1]);
+                    } else {
+#pragma unroll
+                        for (int i = 0; i < 4; ++i) ys[mb][i] = __builtin_fmaf(s, acc[mb][i], ys[mb][i]);
+                    }
+                }
+            }
+        }
+    };
+
+    // Chunk c: its x was loaded during chunk c - 1 and staged into LDS buffer
+    // c % 2 at the end of chunk c - 1; its weights were loaded during chunk
+    // c - 2 into ring slot c % 3. Six chunks per trip so that every buffer
+    // index is compile-time; loads are unconditional (past the end they read
+    // nothing), so the compiler's wait counts are the same on every path.
+    load_x(xr2[0], pr2[0], 0);
+    load_u(ur[0], 0);
+    load_u(ur[1], 1);
+    store_x(xr2[0], pr2[0], xs0, ps0);
+    lds_barrier();
+    auto chunk = [&](auto P, int c) {
+        constexpr int p = decltype(P)::value;
+        load_x(xr2[0], pr2[0], c + 1);
+        load_u(ur[(p + 2) % 3], c + 2);
+        compute(p % 2 ? xs1 : xs0, p % 2 ? ps1 : ps0, ur[p % 3]);
+        store_x(xr2[0], pr2[0], p % 2 ? xs0 : xs1, p % 2 ? ps0 : ps1);  // chunk c + 1
+        lds_barrier();
+    };
+    for (int c = 0; c < nch; c += 6) {
+        chunk(std::integral_constant<int, 0>{}, c);
+        if (c + 1 >= nch) break;
+        chunk(std::integral_constant<int, 1>{}, c + 1);
+        if (c + 2 >= nch) break;
+        chunk(std::integral_constant<int, 2>{}, c + 2);
+        if (c + 3 >= nch) break;
+        chunk(std::integral_constant<int, 3>{}, c + 3);
+        if (c + 4 >= nch) break;
+        chunk(std::integral_constant<int, 4>{}, c + 4);
+        if (c + 5 >= nch) break;
+        chunk(std::integral_constant<int, 5>{}, c + 5);
+    }
+
+    // Partial sums of the S waves of a tile (and source), added in slice order.
+    float *red = reinterpret_cast<float *>(xs);
+    static_assert(kWaves * MB * YV * 64 * 4 == kRedBytes, "reduction buffer");
+#pragma unroll
+    for (int mb = 0; mb < MB; ++mb)
+#pragma unroll
+        for (int i = 0; i < YV; ++i) red[((wave * MB + mb) * YV + i) * 64 + lane] = ys[mb][i];
+    lds_barrier();
+    if (!active || slice != 0 || src != 0) return;
+    const int nc = kTileN * T + r16;
+    if (nc >= N) return;
+#pragma unroll
+    for (int mb = 0; mb < MB; ++mb)
+#pragma unroll
+        for (int i = 0; i < YV; ++i) {
+            float v[NSRC];
+#pragma unroll
+            for (int sr = 0; sr < NSRC; ++sr) {
+                v[sr] = 0.f;
+                for (int sl = 0; sl < S; ++sl)
+                    v[sr] += red[((((tb * NSRC + sr) * S + sl) * MB + mb) * YV + i) * 64 + lane];
+            }
+            const int m = F32X ? TPB * mb + 2 * q + i : 16 * mb + 4 * q + i;
+            if (m < M) y[(size_t)m * N + nc] = NSRC == 2 ? silu_f(v[0]) * v[1] : v[0];
+        }
+}
+
+template <bool F32X, int NSRC, int MB, int GS>
+int launch_gs(st_context *ctx, const void *x, const float *pe, const uint32_t *const *qw, const uint16_t *const *sc,
+              const uint32_t *const *qz, int zoff, float *y, int M, int K, int N, int ntiles, int G, int wpt) {
+    const dim3 grid(G), block(kThreads);
+#define ST_I4MM(KCU_, GW_)                                                                                      \
+    hipLaunchKernelGGL((i4mm_kernel<F32X, NSRC, MB, GS, KCU_, GW_>), grid, block, 0, ctx->stream, x, pe, qw[0], sc[0], \
+                       qz[0], qw[1], sc[1], qz[1], zoff, y, M, K, N, ntiles)
+    // waves per tile and source = 128-k units per chunk (one unit per wave):
+    // 8 (1024-k chunks), 4 or 2
+    if (wpt >= 8)
+        ST_I4MM(8, 1);
+    else if (wpt == 4)
+        ST_I4MM(4, 1);
+    else
+        ST_I4MM(2, 1);
+#undef ST_I4MM
+    return st::launch_check("i4mm_kernel");
+}
+
+template <bool F32X, int NSRC, int MB>
+int launch_mb(st_context *ctx, const void *x, const float *pe, const uint32_t *const *qw, const uint16_t *const *sc,
+              const uint32_t *const *qz, int zoff, float *y, int M, int K, int N, int gs, int ntiles, int G, int wpt) {
+    switch (gs) {
+        case 64: return launch_gs<F32X, NSRC, MB, 64>(ctx, x, pe, qw, sc, qz, zoff, y, M, K, N, ntiles, G, wpt);
+        case 128: return launch_gs<F32X, NSRC, MB, 128>(ctx, x, pe, qw, sc, qz, zoff, y, M, K, N, ntiles, G, wpt);
+        default: return launch_gs<F32X, NSRC, MB, 256>(ctx, x, pe, qw, sc, qz, zoff, y, M, K, N, ntiles, G, wpt);
+    }
+}
+
+template <bool F32X, int NSRC>
+int launch_src(st_context *ctx, const void *x, const float *pe, const uint32_t *const *qw, const uint16_t *const *sc,
+               const uint32_t *const *qz, int zoff, float *y, int M, int K, int N, int gs, int ntiles, int G, int wpt) {
+    // tokens per 16-row block: 8 (f32 x: hi and lo rows) or 16
+    const int mb = (M * (F32X ? 2 : 1) + 15) / 16;
+    return mb <= 1 ? launch_mb<F32X, NSRC, 1>(ctx, x, pe, qw, sc, qz, zoff, y, M, K, N, gs, ntiles, G, wpt)
+                   : launch_mb<F32X, NSRC, 2>(ctx, x, pe, qw, sc, qz, zoff, y, M, K, N, gs, ntiles, G, wpt);
+}
+
+}  // namespace
+
+namespace st {
+
+// Arguments are checked by the entry points (tiled weights, no act-order,
+// M <= 16, K % 128 == 0, K % group_size == 0, N % 8 == 0, alignment, 32-bit
+// offsets).
+int int4_mm_f16(st_context *ctx, const void *x, bool x_f32, const uint32_t *const qw[2], const uint16_t *const sc[2],
+                const uint32_t *const qz[2], int zoff, float *y, int M, int K, int N, int gs, int nsrc) {
+    const int ntiles = (N + kTileN - 1) / kTileN;
+    const int maxt = kMaxTilesPerWg / nsrc;  // tiles per workgroup: each tile (and source) keeps >= 2 waves
+    const int G = std::max(std::min(ctx->num_cus, ntiles), (ntiles + maxt - 1) / maxt);
+    const int tbmax = (ntiles + G - 1) / G;
+    int wpt = 2;  // waves per tile and source: a power of two, wpt * nsrc * tbmax <= 16
+    while (wpt < 8 && 2 * wpt * nsrc * tbmax <= kWaves) wpt *= 2;
+    if (wpt * nsrc * tbmax > kWaves) return fail(ST_ERR_SHAPE, "int4_mm_f16: %d tiles per workgroup", tbmax);
+    const void *xa = x;
+    const float *pe = nullptr;
+    if (x_f32) {  // the pre-pass writes [2M, K] f16 rows and [M, K / 128] factors into the workspace
+        const size_t xbytes = ((size_t)2 * M * K * 2 + 255) & ~size_t(255);
+        if (!ctx->ws || xbytes + (size_t)M * (K / 128) * 4 > ctx->ws_bytes)
+            return fail(ST_ERR_WORKSPACE, "int4_mm_f16: workspace below %zu B", xbytes + (size_t)M * (K / 128) * 4);
+        _Float16 *xp = reinterpret_cast<_Float16 *>(ctx->ws);
+        pe = reinterpret_cast<const float *>(reinterpret_cast<const char *>(ctx->ws) + xbytes);
+        const int groups = M * (K / 128);
+        hipLaunchKernelGGL(i4mm_prep_kernel, dim3((groups + 15) / 16), dim3(256), 0, ctx->stream,
+                           static_cast<const float *>(x), xp, const_cast<float *>(pe), M, K);
+        if (int rc = launch_check("i4mm_prep_kernel")) return rc;
+        xa = xp;
+    }
+    if (nsrc == 2)
+        return x_f32 ? launch_src<true, 2>(ctx, xa, pe, qw, sc, qz, zoff, y, M, K, N, gs, ntiles, G, wpt)
+                     : launch_src<false, 2>(ctx, xa, pe, qw, sc, qz, zoff, y, M, K, N, gs, ntiles, G, wpt);
+    return x_f32 ? launch_src<true, 1>(ctx, xa, pe, qw, sc, qz, zoff, y, M, K, N, gs, ntiles, G, wpt)
+                 : launch_src<false, 1>(ctx, xa, pe, qw, sc, qz, zoff, y, M, K, N, gs, ntiles, G, wpt);
+}
+
+}  // namespace st

@@ -66,7 +66,24 @@ __global__ __launch_bounds__(256) void repack8_kernel(const int8_t *__restrict__
     reinterpret_cast<uint4 *>(out)[idx] = *reinterpret_cast<const uint4 *>(w + (size_t)n * K + k0);
 }
 
+// The GPTQ entry points take the f16-MFMA kernel (tiled weights, no
+// act-order, f32 or f16 x) from this many tokens on, when N has more
+// 16-column tiles than the GPU has CUs (as measured on configs[4]'s shapes:
+// at 16 tokens q|k|v 12.1 -> 11.2 us, gate/up 20.2 -> 18.0, lm_head 134 -> 83;
+// with fewer tiles or tokens the integer-limb kernels are faster).
+constexpr int kI4mmMinM = 12;
+
+bool use_i4mm(const st_context *ctx, const QmvParams &p, bool tiled, int xm) {
+    const int ntiles = (p.N + kTileN - 1) / kTileN;
+    const int min_m = std::max(2, st::qmv::env_int("ST_I4MM_MIN_M", kI4mmMinM));
+    const int min_tiles = st::qmv::env_int("ST_I4MM_MIN_TILES", ctx->num_cus + 1);
+    return tiled && !p.perm && (xm == XM_F32 || xm == XM_F16) && p.M <= 16 && p.M >= min_m && ntiles >= min_tiles &&
+           p.K % 128 == 0 && (size_t)ntiles * kTileN * p.K / 2 < (size_t(1) << 31);
+}
+
 int launch_i4(st_context *ctx, QmvParams &p, bool tiled, int nsrc, int xm) {
+    if (use_i4mm(ctx, p, tiled, xm))
+        return st::int4_mm_f16(ctx, p.x, xm == XM_F32, p.qw, p.sc, p.qz, p.zoff, p.y, p.M, p.K, p.N, p.gs, nsrc);
     p.units = p.K / p.gs;
     p.ntiles = (p.N + kTileN - 1) / kTileN;
     // the tiled kernels address the weights with 32-bit buffer offsets

@@ -635,7 +635,7 @@ __global__ __launch_bounds__((64 * (CM == 3 ? kChunkWaves<NSRC, MB> : kMaxWavesF
         for (int mb = 0; mb < MB; ++mb) {
             const int m = min(mb * 4 + q, M - 1);
             const u32x4 es = s_es[ui * M + m];
-            const float em = __builtin_bit_cast(float, es.x);
+            const float em = __builtin_bit_cast(float, (unsigned)es.x);  // (a prvalue: bit_cast of a vector element lvalue reads element 0)
             const int nh = (int)es.y, nl = (int)es.z;
 #pragma unroll
             for (int src = 0; src < NSRC; ++src) {

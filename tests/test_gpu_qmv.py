@@ -715,3 +715,124 @@ def test_int8_mm_f16_graph_replay(gpu, orc):
         g.replay()
         torch.cuda.synchronize()
         assert torch.equal(y, eager)
+
+
+def _force_i4mm(monkeypatch):
+    monkeypatch.setenv("ST_I4MM_MIN_M", "2")
+    monkeypatch.setenv("ST_I4MM_MIN_TILES", "1")
+
+
+def _gate_up(gpu, wg, wu, x, dtype=torch.float32):
+    xt = torch.from_numpy(np.ascontiguousarray(x)).to(gpu.device)
+    if dtype == torch.float16:
+        xt = xt.half()
+    y = torch.empty(x.shape[0], wg.N, device=gpu.device)
+    M.fused_gate_up_silu(gpu, xt, wg.qweight, wg.scales, wu.qweight, wu.scales, y, wg.K, wg.N, wg.group_size,
+                         gate_qz=wg.qzeros, up_qz=wu.qzeros, flags=wg.flags)
+    torch.cuda.synchronize()
+    return y.cpu().numpy()
+
+
+@pytest.mark.parametrize("Mr,K,N,gs,zeros,f16,dual", [
+    (2, 128, 64, 128, False, False, False),     # one unit, one tile
+    (5, 384, 72, 64, True, False, False),       # group 64, ragged last tile
+    (16, 2560, 6144, 128, False, False, False),  # configs[4] q|k|v at batch 16
+    (16, 9728, 2560, 128, False, False, False),  # configs[4] down: 160 tiles, 76 units
+    (9, 4096, 520, 256, True, False, False),    # group 256, two 16-row blocks
+    (12, 1024, 1000, 128, True, True, False),   # f16 x
+    (3, 256, 36880, 128, False, False, False),  # 2305 tiles: more workgroups than CUs
+    (16, 2560, 9728, 128, False, False, True),  # configs[4] gate/up at batch 16
+    (6, 1536, 776, 64, True, True, True),       # gate/up, f16 x, zeros, group 64
+])
+def test_int4_mm_f16(gpu, orc, Mr, K, N, gs, zeros, f16, dual, monkeypatch):
+    """2..16 tokens on tiled GPTQ weights: the f16-MFMA kernel ((q - z)
+    exact in f16, f32 x as two f16 rows per 128-k block scaled by a power of
+    two, exact products, f32 sums and per-group scaling) against the f64
+    oracle, and against the integer-limb kernels. (The entry points choose
+    it for 12+ tokens and more tiles than CUs; forced here.)"""
+    _force_i4mm(monkeypatch)
+    xd = np.float16 if f16 else np.float32
+    c = orc.gptq_case(150 + Mr, K, N, gs, zeros=zeros, M=Mr, x_dtype=xd)
+    w = up(gpu, c)
+    dt = torch.float16 if f16 else torch.float32
+    ref = orc.gptq_matvec_f64(c["x"], c["qweight"], c["scales"], K, N, gs, qzeros=c["qzeros"])
+    if dual:
+        c2 = orc.gptq_case(250 + Mr, K, N, gs, zeros=zeros)
+        w2 = up(gpu, c2)
+        ref = orc.silu_gate_f64(ref, orc.gptq_matvec_f64(c["x"], c2["qweight"], c2["scales"], K, N, gs,
+                                                         qzeros=c2["qzeros"]))
+        run = lambda: _gate_up(gpu, w, w2, c["x"], dt)
+    else:
+        run = lambda: run_matvec(gpu, w, c["x"], dt)
+    y = run()
+    e = orc.rel_l2(y, ref)
+    print(f"int4 f16-MFMA M={Mr} K={K} N={N} gs={gs} dual={dual} rel-L2 {e:.3e}")
+    assert np.isfinite(y).all() and e < 1e-5
+    monkeypatch.setenv("ST_I4MM_MIN_M", "99")
+    assert orc.rel_l2(run(), ref) < TOL
+
+
+def test_int4_mm_f16_integer_exact(gpu, orc, monkeypatch):
+    """Integer x, unit scales, zeros: every product and partial sum is an
+    integer below 2^24, so y equals the exact integer result bit for bit
+    (pins the nibble order, the zero nibble and the row/column mapping)."""
+    _force_i4mm(monkeypatch)
+    Mr, K, N, gs = 11, 1152, 136, 128
+    c = orc.gptq_case(170, K, N, gs, zeros=True)
+    rng = np.random.default_rng(3)
+    x = rng.integers(-3, 4, size=(Mr, K)).astype(np.float32)
+    c["scales"] = np.ones_like(c["scales"])
+    w = up(gpu, c)
+    y = run_matvec(gpu, w, x)
+    qw, qz = c["qweight"], c["qzeros"]
+    q = np.stack([(qw >> (4 * j)) & 0xF for j in range(8)], axis=1).reshape(K, N).astype(np.int64)
+    z = np.stack([(qz >> (4 * j)) & 0xF for j in range(8)], axis=2).reshape(K // gs, N).astype(np.int64)
+    Wd = q - np.repeat(z, gs, axis=0)
+    assert np.array_equal(y, (x.astype(np.int64) @ Wd).astype(np.float32))
+
+
+def test_int4_mm_f16_wide_range_x(gpu, orc, monkeypatch):
+    """f32 x spanning 1e-30 .. 1e30 across 128-k blocks (outside f16's
+    range): the per-block power-of-two split keeps the bar."""
+    _force_i4mm(monkeypatch)
+    Mr, K, N = 7, 2048, 264
+    c = orc.gptq_case(171, K, N, 128, M=Mr)
+    blk = np.repeat(10.0 ** np.linspace(-30, 30, K // 128), 128).astype(np.float32)
+    x = (c["x"] * blk).astype(np.float32)
+    w = up(gpu, c)
+    y = run_matvec(gpu, w, x)
+    ref = orc.gptq_matvec_f64(x, c["qweight"], c["scales"], K, N, 128)
+    assert np.isfinite(y).all() and orc.rel_l2(y, ref) < 1e-5
+
+
+def test_int4_mm_f16_graph_replay(gpu, orc, monkeypatch):
+    """Gate/up and matvec on the f16-MFMA kernel under graph capture: every
+    replay equals the eager result bit for bit."""
+    _force_i4mm(monkeypatch)
+    Mr, K, N = 16, 2560, 1040
+    c = orc.gptq_case(172, K, N, 128, M=Mr)
+    c2 = orc.gptq_case(173, K, N, 128)
+    w, w2 = up(gpu, c), up(gpu, c2)
+    x = torch.from_numpy(c["x"]).cuda()
+    y = torch.empty(Mr, N, device="cuda")
+    h = torch.empty(Mr, N, device="cuda")
+
+    def calls():
+        M.gptq_matvec(gpu, "t", x, w.qweight, w.scales, y, K, N, 128, None, None, w.flags)
+        M.fused_gate_up_silu(gpu, x, w.qweight, w.scales, w2.qweight, w2.scales, h, K, N, 128, flags=w.flags)
+
+    calls()
+    torch.cuda.synchronize()
+    ye, he = y.clone(), h.clone()
+    s = torch.cuda.Stream()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.stream(s):
+        with torch.cuda.graph(g, stream=s):
+            calls()
+    for _ in range(3):
+        y.zero_()
+        h.zero_()
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(y, ye) and torch.equal(h, he)
