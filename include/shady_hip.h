@@ -29,9 +29,10 @@
  *  - A context is not thread-safe (the reference serialises through
  *    `&mut GpuContext`).
  *  - No call allocates. The context's workspace (st_context_reserve_workspace)
- *    holds the prefill GEMM's pre-processed A and split-K partials, and the
+ *    holds the prefill GEMM's pre-processed A and split-K partials, the
  *    split-K partials of multi-token (M > 1) decode calls on linears with few
- *    16-column tiles; one-token decode calls use none. Calls on one context
+ *    16-column tiles, and the split f32 x of 12-16-token GPTQ calls on wide
+ *    linears; one-token decode calls use none. Calls on one context
  *    are ordered by its stream, so they never overlap on it.
  */
 #ifndef SHADY_HIP_H
@@ -125,7 +126,12 @@ int st_flush(st_context *ctx);
  * Requires K % group_size == 0, group_size in {64, 128, 256}, N % 8 == 0,
  * 1 <= M <= 32, 16-byte aligned qweight and x. Accumulation: exact integer
  * products of the nibbles with a 3 x 8-bit split of x scaled by a power of
- * two per group, f32 across groups (rel-L2 vs f64 ~1e-7). */
+ * two per group, f32 across groups (rel-L2 vs f64 ~1e-7). For 12-16 tokens
+ * (per 16-token block) on tiled weights without perm, when N has more
+ * 16-column tiles than the GPU has CUs: f16 MFMA on exact (q - z) and x (f16
+ * x as is; f32 x split once into two f16 parts per 128 k, by a pre-pass that
+ * uses the context workspace), f32 sums, rel-L2 vs f64 ~1e-7. The same rule
+ * applies to st_gptq_i4_gate_up_silu. */
 int st_gptq_i4_matvec(st_context *ctx, const void *x, int x_dtype,
                       const uint32_t *qweight, const uint16_t *scales,
                       const uint32_t *qzeros, const int32_t *perm, float *y,
@@ -203,7 +209,10 @@ int st_gptq_i4_gemm(st_context *ctx, const uint16_t *a, const uint32_t *qweight,
 /* y[M, N] = x[M, K] . (w[N, K]^T * scale[N]), int8 symmetric per output
  * channel. No reference counterpart. x in x_dtype (ST_F16 or ST_F32),
  * 1 <= M <= 32, K % 128 == 0, N % 4 == 0. flags: ST_FLAG_TILED when w is in
- * the layout of st_int8_repack (else row-major int8[N, K]). */
+ * the layout of st_int8_repack (else row-major int8[N, K]). Two or more
+ * tokens with f16 x on tiled weights run on f16 MFMA (every product exact,
+ * f32 sums; the weights are read once for all tokens); otherwise exact
+ * integer products with a split of x as for st_gptq_i4_matvec. */
 int st_int8_matvec(st_context *ctx, const void *x, int x_dtype, const int8_t *w,
                    const float *scale, float *y, int M, int K, int N, uint32_t flags);
 
