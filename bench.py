@@ -412,7 +412,7 @@ def bench_stack(torch, dev, gpu, Mdl, gen, args):
         out[f"batch{Mb}"] = {"ms_per_token_step": round(ms, 4), "tokens_per_s": round(Mb / (ms * 1e-3), 1),
                              "GB/s": round(tok_bytes / (ms * 1e-3) / 1e9, 1),
                              "hbm_frac": round(tok_bytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
-                             "kernels_per_step": 4 * L + 1, "qkv": "one concatenated linear"}
+                             "linear_calls_per_step": 4 * L + 1, "qkv": "one concatenated linear"}
     # Prefill of a 512-token prompt through the same weights with the GEMM
     # (f16 activations and outputs; q, k, v, o, gate, up, down per layer),
     # then the lm_head for the last token only, as a prefill does.

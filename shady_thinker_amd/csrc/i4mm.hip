@@ -9,8 +9,9 @@
 //    f16 1024 bias: 1024 + q, minus 1024 + z). f16 x is used as is. f32 x is
 //    split once, by a pre-pass into the context workspace, per token and per
 //    128 k: x 2^-e (2^e just above the block's largest |x|) = hi + lo, two
-//    f16 rows of the MFMA A operand (about 22 significant bits). Every product is exact in f32; each 64 (or 128) k
-//    block sums into a fresh accumulator that is then scaled by s 2^e in f32.
+//    f16 rows of the MFMA A operand (about 22 significant bits). Every
+//    product is exact in f32; each 64 (or 128) k block sums into a fresh
+//    accumulator that is then scaled by s 2^e in f32.
 //  * Every weight is read from HBM once for all tokens (the integer-limb
 //    matvec kernels grow their per-token staging and epilogue work with M).
 //  * Work split as in i8mm.hip: one workgroup per CU owns a run of 16-column
