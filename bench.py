@@ -184,7 +184,7 @@ def main():
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:
         print("bench.py: this build measures one GPU; multi-GPU runs are not part of it "
-              "(the decode matvec would shard column-parallel, see DESIGN.md)", file=sys.stderr)
+              "(the decode matvec would shard column-parallel over N, with no exchange between GPUs)", file=sys.stderr)
         sys.exit(2)
 
     import torch

@@ -30,7 +30,8 @@ FLAGS = [
     "-Wall",
     "-Wno-unused-function",
     "-Wno-unused-variable",
-    # Packed-FP32 VALU forms are kept out of every kernel.
+    # Packed-FP32 VALU forms are kept out of every kernel (some of their forms
+    # have given wrong results on this hardware).
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
     "-I", os.path.join(ROOT, "include"),
     "-I", CSRC,
