@@ -361,27 +361,23 @@ def bench_stack(torch, dev, gpu, Mdl, gen, args):
     (hidden 2560, 32 q / 8 kv heads of 128, intermediate 9728, vocab 151936),
     every linear GPTQ int4 g128 (lm_head included), random-init packed
     weights (2.07 GB: each token streams them from HBM). A token = per layer
-    q, k, v, o, fused gate/up (silu(g)*u) and down on it, then the lm_head;
-    captured as one HIP graph and replayed; batch 1 and 16. Attention and
-    norms are outside the path, so activations are synthetic and fixed."""
+    DecoderLinears.decode (q|k|v, o, fused gate/up emitting silu(g)*u, down
+    on it), then the lm_head; captured as one HIP graph and replayed; batch
+    1 and 16. Attention and norms are outside the path, so activations are
+    synthetic and fixed."""
     H, Q, KV, I, V, L = 2560, 4096, 1024, 9728, 151936, 36
     TF = sta_flags_tiled()
-    layers = []
-    for _ in range(L):
-        layers.append({"q": make_gptq(torch, dev, H, Q, gen, gpu), "k": make_gptq(torch, dev, H, KV, gen, gpu),
-                       "v": make_gptq(torch, dev, H, KV, gen, gpu), "o": make_gptq(torch, dev, Q, H, gen, gpu),
-                       "g": make_gptq(torch, dev, H, I, gen, gpu), "u": make_gptq(torch, dev, H, I, gen, gpu),
-                       "d": make_gptq(torch, dev, I, H, gen, gpu)})
-    lm = make_gptq(torch, dev, H, V, gen, gpu)
-    # q, k and v read the same x: one concatenated linear per layer (upload-time
-    # GptqWeight.cat; values unchanged), one launch instead of three
     import shady_thinker_amd as sta
 
-    for w in layers:
-        parts = [sta.GptqWeight(w[n][0], w[n][1], None, None, H, d, GS, TF) for n, d in (("q", Q), ("k", KV), ("v", KV))]
-        qkv = sta.GptqWeight.cat(parts)
-        w["qkv"] = (qkv.qweight, qkv.scales)
-        del w["q"], w["k"], w["v"]
+    def gw(k, n):
+        qw, sc = make_gptq(torch, dev, k, n, gen, gpu)
+        return sta.GptqWeight(qw, sc, None, None, k, n, GS, TF)
+
+    # One DecoderLinears per layer (q, k and v concatenated at construction:
+    # GptqWeight.cat, values unchanged, one launch instead of three).
+    layers = [sta.DecoderLinears(gw(H, Q), gw(H, KV), gw(H, KV), gw(Q, H), gw(H, I), gw(H, I), gw(I, H))
+              for _ in range(L)]
+    lm = make_gptq(torch, dev, H, V, gen, gpu)
     per_layer = (decode_bytes(H, Q, 4, Q) + 2 * decode_bytes(H, KV, 4, KV) + decode_bytes(Q, H, 4, H) +
                  decode_bytes(H, 2 * I, 4, I) + decode_bytes(I, H, 4, H))
     out = {"layers": L, "weights_GB": None}
@@ -396,11 +392,8 @@ def bench_stack(torch, dev, gpu, Mdl, gen, args):
         logits = torch.empty(Mb, V, device=dev)
 
         def token(i):
-            for w in layers:
-                Mdl.gptq_matvec(gpu, "qkv_proj", x, w["qkv"][0], w["qkv"][1], yqkv, H, Q + 2 * KV, GS, flags=TF)
-                Mdl.gptq_matvec(gpu, "o_proj", attn, w["o"][0], w["o"][1], yo, Q, H, GS, flags=TF)
-                Mdl.fused_gate_up_silu(gpu, x, w["g"][0], w["g"][1], w["u"][0], w["u"][1], h, H, I, GS, flags=TF)
-                Mdl.gptq_matvec(gpu, "down_proj", h, w["d"][0], w["d"][1], yd, I, H, GS, flags=TF)
+            for layer in layers:
+                layer.decode(gpu, x, attn, yqkv, yo, h, yd)
             Mdl.gptq_matvec(gpu, "lm_head", x, lm[0], lm[1], logits, H, V, GS, flags=TF)
 
         iters = max(10, min(50, args.steps // 4))
@@ -414,25 +407,23 @@ def bench_stack(torch, dev, gpu, Mdl, gen, args):
                              "hbm_frac": round(tok_bytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
                              "linear_calls_per_step": 4 * L + 1, "qkv": "one concatenated linear"}
     # Prefill of a 512-token prompt through the same weights with the GEMM
-    # (f16 activations and outputs; q, k, v, o, gate, up, down per layer),
-    # then the lm_head for the last token only, as a prefill does.
+    # (DecoderLinears.prefill: f16 activations and outputs; q|k|v, o, gate,
+    # up, and down on silu(gate) * up fused into the GEMM's A pass), then the
+    # lm_head for the last token only, as a prefill does.
     P = 512
     xa = torch.randn(P, H, device=dev, generator=gen).half()
     aa = torch.randn(P, Q, device=dev, generator=gen).half()
-    ha = torch.randn(P, I, device=dev, generator=gen).half()
     cq = torch.empty(P, Q + 2 * KV, device=dev, dtype=torch.float16)
-    ch = torch.empty(P, H, device=dev, dtype=torch.float16)
-    ci = torch.empty(P, I, device=dev, dtype=torch.float16)
+    co = torch.empty(P, H, device=dev, dtype=torch.float16)
+    cg = torch.empty(P, I, device=dev, dtype=torch.float16)
+    cu = torch.empty(P, I, device=dev, dtype=torch.float16)
+    cd = torch.empty(P, H, device=dev, dtype=torch.float16)
     xl = torch.randn(1, H, device=dev, generator=gen)
     logits1 = torch.empty(1, V, device=dev)
 
     def prefill(i):
-        for w in layers:
-            Mdl.gptq_gemm(gpu, xa, w["qkv"][0], w["qkv"][1], cq, H, Q + 2 * KV, GS, None, None, TF)
-            Mdl.gptq_gemm(gpu, aa, w["o"][0], w["o"][1], ch, Q, H, GS, None, None, TF)
-            Mdl.gptq_gemm(gpu, xa, w["g"][0], w["g"][1], ci, H, I, GS, None, None, TF)
-            Mdl.gptq_gemm(gpu, xa, w["u"][0], w["u"][1], ci, H, I, GS, None, None, TF)
-            Mdl.gptq_gemm(gpu, ha, w["d"][0], w["d"][1], ch, I, H, GS, None, None, TF)
+        for layer in layers:
+            layer.prefill(gpu, xa, aa, cq, co, cg, cu, cd)
         Mdl.gptq_matvec(gpu, "lm_head", xl, lm[0], lm[1], logits1, H, V, GS, flags=TF)
 
     ms = Replayer(torch, prefill, 1).run(max(3, min(10, args.steps // 20)), 1)

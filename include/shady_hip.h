@@ -204,6 +204,17 @@ int st_gptq_i4_gemm(st_context *ctx, const uint16_t *a, const uint32_t *qweight,
                     void *c, int c_dtype, int M, int K, int N, int group_size,
                     uint32_t flags);
 
+/* Prefill GEMM on silu(gate) * up: C[M, N] = (silu(gate) * up)[M, K] .
+ * dequant(W), gate and up f16 [M, K], silu(v) = v / (1 + exp(-v)) in f32,
+ * the product rounded once to f16. The M-token form of
+ * Model::fused_silu_gptq_down (src/model.rs:383-408, fused_silu_gptq(_4t).wgsl),
+ * which the reference runs one token at a time (src/model.rs:803-811). Other
+ * arguments as st_gptq_i4_gemm. */
+int st_gptq_i4_silu_gemm(st_context *ctx, const uint16_t *gate, const uint16_t *up,
+                         const uint32_t *qweight, const uint16_t *scales, const uint32_t *qzeros,
+                         const int32_t *perm, void *c, int c_dtype, int M, int K, int N,
+                         int group_size, uint32_t flags);
+
 /* ------------------------------------------------------------- INT8 */
 
 /* y[M, N] = x[M, K] . (w[N, K]^T * scale[N]), int8 symmetric per output

@@ -11,11 +11,13 @@ from .model import (  # noqa: F401
     bf16_matvec,
     fused_gate_up_silu,
     fused_silu_gptq_down,
+    fused_silu_gptq_gemm,
     gptq_dequant,
     gptq_gemm,
     gptq_matvec,
     int8_matvec,
     linear,
 )
+from .layer import DecoderLinears  # noqa: F401
 from .loader import load_gptq_checkpoint, read_gptq_checkpoint  # noqa: F401
 from .weights import GptqWeight, Int8Weight, QuantConfig  # noqa: F401

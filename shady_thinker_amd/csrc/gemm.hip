@@ -350,13 +350,30 @@ __device__ __forceinline__ u32x4 to_b_order(u32x4 a) {
 // GEMM A operand: A'[m][8c + i] = A[m][perm[8c + o(i)]] (perm = identity
 // when NULL), o = (0,4,1,5,2,6,3,7): the act-order gather and the B
 // register order of each 8-k chunk in one pass. One workgroup per row, the
-// row staged in LDS.
-__global__ __launch_bounds__(256) void prep_a_kernel(const _Float16 *__restrict__ A, const int32_t *__restrict__ perm,
-                                                     _Float16 *__restrict__ out, int K) {
+// row staged in LDS. With U non-NULL the row is first h = silu(A) * U,
+// silu(v) = v / (1 + exp(-v)) (fused_silu_gptq.wgsl:19-21) in f32, rounded
+// once to f16: the fused silu.down of the reference's MLP
+// (src/model.rs:803-811) for a block of tokens.
+__global__ __launch_bounds__(256) void prep_a_kernel(const _Float16 *__restrict__ A, const _Float16 *__restrict__ U,
+                                                     const int32_t *__restrict__ perm, _Float16 *__restrict__ out,
+                                                     int K) {
     extern __shared__ _Float16 row[];
     const size_t base = (size_t)blockIdx.x * K;
-    for (int k = threadIdx.x * 8; k < K; k += 256 * 8)
-        *reinterpret_cast<u32x4 *>(&row[k]) = *reinterpret_cast<const u32x4 *>(A + base + k);
+    for (int k = threadIdx.x * 8; k < K; k += 256 * 8) {
+        if (U) {
+            const half8 g = *reinterpret_cast<const half8 *>(A + base + k);
+            const half8 u = *reinterpret_cast<const half8 *>(U + base + k);
+            half8 h;
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+                const float gv = (float)g[e];
+                h[e] = (_Float16)(__fdividef(gv, 1.0f + __expf(-gv)) * (float)u[e]);
+            }
+            *reinterpret_cast<half8 *>(&row[k]) = h;
+        } else {
+            *reinterpret_cast<u32x4 *>(&row[k]) = *reinterpret_cast<const u32x4 *>(A + base + k);
+        }
+    }
     __syncthreads();
     for (int k = threadIdx.x * 8; k < K; k += 256 * 8) {
         u32x4 v;
@@ -484,29 +501,33 @@ Split plan_split(st_context *ctx, int M, int K, int N, int cb, size_t ws_used) {
 
 }  // namespace
 
-extern "C" int st_gptq_i4_gemm(st_context *ctx, const uint16_t *a, const uint32_t *qweight, const uint16_t *scales,
-                               const uint32_t *qzeros, const int32_t *perm, void *c, int c_dtype, int M, int K, int N,
-                               int group_size, uint32_t flags) {
-    if (!ctx || !a || !qweight || !scales || !c) return st::fail(ST_ERR_INVALID, "st_gptq_i4_gemm: NULL argument");
+namespace {
+
+// The prefill GEMM behind both entry points: u == NULL for a . dequant(W),
+// else silu(a) * u . dequant(W).
+int gemm_impl(const char *fn, st_context *ctx, const uint16_t *a, const uint16_t *u, const uint32_t *qweight,
+              const uint16_t *scales, const uint32_t *qzeros, const int32_t *perm, void *c, int c_dtype, int M, int K,
+              int N, int group_size, uint32_t flags) {
+    if (!ctx || !a || !qweight || !scales || !c) return st::fail(ST_ERR_INVALID, "%s: NULL argument", fn);
     if (group_size != 64 && group_size != 128 && group_size != 256)
-        return st::fail(ST_ERR_SHAPE, "st_gptq_i4_gemm: group_size %d not in {64,128,256}", group_size);
+        return st::fail(ST_ERR_SHAPE, "%s: group_size %d not in {64,128,256}", fn, group_size);
     if (M < 1 || K <= 0 || K % KT || K % group_size || N <= 0 || N % 8)
-        return st::fail(ST_ERR_SHAPE, "st_gptq_i4_gemm: M=%d K=%d N=%d (K %% 128, K %% group_size, N %% 8)", M, K, N);
-    if (c_dtype != ST_F32 && c_dtype != ST_F16) return st::fail(ST_ERR_INVALID, "st_gptq_i4_gemm: c_dtype %d", c_dtype);
-    if (!st::aligned16(a) || !st::aligned16(qweight))
-        return st::fail(ST_ERR_ALIGN, "st_gptq_i4_gemm: a and qweight must be 16-byte aligned");
+        return st::fail(ST_ERR_SHAPE, "%s: M=%d K=%d N=%d (K %% 128, K %% group_size, N %% 8)", fn, M, K, N);
+    if (c_dtype != ST_F32 && c_dtype != ST_F16) return st::fail(ST_ERR_INVALID, "%s: c_dtype %d", fn, c_dtype);
+    if (!st::aligned16(a) || !st::aligned16(u) || !st::aligned16(qweight))
+        return st::fail(ST_ERR_ALIGN, "%s: activations and qweight must be 16-byte aligned", fn);
     if ((size_t)M * K * 2 > 0x7FFFFFFFu || (size_t)K / 8 * ((N + 15) / 16 * 16) * 4 > 0x7FFFFFFFu)
-        return st::fail(ST_ERR_SHAPE, "st_gptq_i4_gemm: A or qweight above 2 GiB (M=%d K=%d N=%d); split M or N", M, K,
-                        N);
-    if (K > 32768) return st::fail(ST_ERR_SHAPE, "st_gptq_i4_gemm: K=%d above 32768", K);
+        return st::fail(ST_ERR_SHAPE, "%s: A or qweight above 2 GiB (M=%d K=%d N=%d); split M or N", fn, M,
+                        K, N);
+    if (K > 32768) return st::fail(ST_ERR_SHAPE, "%s: K=%d above 32768", fn, K);
     const size_t need = (size_t)M * K * sizeof(_Float16);
     if (need > ctx->ws_bytes)
-        return st::fail(ST_ERR_WORKSPACE, "st_gptq_i4_gemm: needs %zu B of workspace for A (st_context_reserve_workspace)",
+        return st::fail(ST_ERR_WORKSPACE, "%s: needs %zu B of workspace for A (st_context_reserve_workspace)", fn,
                         need);
-    if (perm && !st::aligned16(perm)) return st::fail(ST_ERR_ALIGN, "st_gptq_i4_gemm: perm must be 16-byte aligned");
+    if (perm && !st::aligned16(perm)) return st::fail(ST_ERR_ALIGN, "%s: perm must be 16-byte aligned", fn);
     _Float16 *A = reinterpret_cast<_Float16 *>(ctx->ws);
     hipLaunchKernelGGL(prep_a_kernel, dim3(M), dim3(256), (size_t)K * sizeof(_Float16), ctx->stream,
-                       reinterpret_cast<const _Float16 *>(a), perm, A, K);
+                       reinterpret_cast<const _Float16 *>(a), reinterpret_cast<const _Float16 *>(u), perm, A, K);
     if (int rc = st::launch_check("prep_a_kernel")) return rc;
     const int zoff = (flags & ST_FLAG_ZEROS_PLUS_ONE) ? 1 : 0;
     const bool f16out = c_dtype == ST_F16;
@@ -515,4 +536,21 @@ extern "C" int st_gptq_i4_gemm(st_context *ctx, const uint16_t *a, const uint32_
     if (flags & ST_FLAG_TILED)
         return launch_tiled<true>(ctx, A, qweight, scales, qzeros, zoff, c, f16out, M, K, N, group_size, cb, sp);
     return launch_tiled<false>(ctx, A, qweight, scales, qzeros, zoff, c, f16out, M, K, N, group_size, cb, sp);
+}
+
+}  // namespace
+
+extern "C" int st_gptq_i4_gemm(st_context *ctx, const uint16_t *a, const uint32_t *qweight, const uint16_t *scales,
+                               const uint32_t *qzeros, const int32_t *perm, void *c, int c_dtype, int M, int K, int N,
+                               int group_size, uint32_t flags) {
+    return gemm_impl("st_gptq_i4_gemm", ctx, a, nullptr, qweight, scales, qzeros, perm, c, c_dtype, M, K, N, group_size,
+                     flags);
+}
+
+extern "C" int st_gptq_i4_silu_gemm(st_context *ctx, const uint16_t *gate, const uint16_t *up, const uint32_t *qweight,
+                                    const uint16_t *scales, const uint32_t *qzeros, const int32_t *perm, void *c,
+                                    int c_dtype, int M, int K, int N, int group_size, uint32_t flags) {
+    if (!up) return st::fail(ST_ERR_INVALID, "st_gptq_i4_silu_gemm: NULL argument");
+    return gemm_impl("st_gptq_i4_silu_gemm", ctx, gate, up, qweight, scales, qzeros, perm, c, c_dtype, M, K, N,
+                     group_size, flags);
 }

@@ -98,6 +98,24 @@ def gptq_gemm(gpu, a, qweight, scales, c, k: int, n: int, group_size: int = 128,
          k, n, group_size, flags)
 
 
+def fused_silu_gptq_gemm(gpu, gate_out, up_out, down_qw, down_sc, output, k: int, n: int, group_size: int = 128,
+                         qzeros=None, perm=None, flags: int = 0) -> None:
+    """output[M, n] = (silu(gate_out) * up_out)[M, k] . dequant(W): the
+    M-token form of fused_silu_gptq_down (src/model.rs:383-408) through the
+    prefill GEMM; gate_out and up_out f16, output float32 or float16."""
+    import torch
+
+    m = _rows(gate_out, k)
+    if up_out.shape != gate_out.shape or gate_out.dtype != torch.float16 or up_out.dtype != torch.float16:
+        raise TypeError("gate_out and up_out: float16 tensors of one shape")
+    cd = {torch.float32: ST_F32, torch.float16: ST_F16}.get(output.dtype)
+    if cd is None:
+        raise TypeError(f"gemm output dtype {output.dtype}")
+    gpu.sync_stream()
+    call("st_gptq_i4_silu_gemm", gpu.handle, ptr(gate_out), ptr(up_out), ptr(down_qw), ptr(down_sc), ptr(qzeros),
+         ptr(perm), ptr(output), cd, m, k, n, group_size, flags)
+
+
 def bf16_matvec(gpu, x, w, y, k: int, n: int) -> None:
     """y[M, n] = x[M, k] . w^T, w bf16 [n, k] (Model::bf16_lm_head,
     src/model.rs:455-468 / bf16_matvec.wgsl). x f32 or f16, y f32, M <= 8."""

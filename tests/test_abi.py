@@ -44,7 +44,7 @@ def test_null_arguments_are_rejected():
     assert L.st_context_create(0, None) == 1  # ST_ERR_INVALID
     assert b"NULL" in L.st_last_error()
     for fn, nargs in [("st_gptq_i4_matvec", 13), ("st_gptq_i4_silu_matvec", 13), ("st_gptq_i4_gate_up_silu", 16),
-                      ("st_int8_matvec", 10), ("st_gptq_i4_gemm", 13), ("st_gptq_i4_dequant", 11),
+                      ("st_int8_matvec", 10), ("st_gptq_i4_gemm", 13), ("st_gptq_i4_silu_gemm", 14), ("st_gptq_i4_dequant", 11),
                       ("st_gptq_i4_act_order", 8), ("st_bf16_matvec", 8), ("st_int8_repack", 5),
                       ("st_gptq_i4_repack", 6)]:
         args = [None] * nargs

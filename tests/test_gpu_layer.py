@@ -1,0 +1,128 @@
+"""GPU tests of the M-token callers: the fused silu.down prefill GEMM
+(st_gptq_i4_silu_gemm) and DecoderLinears (one layer's projections for
+decode and for prefill), against the f64 oracle through the C ABI."""
+import numpy as np
+import pytest
+import torch
+
+import shady_thinker_amd as sta
+from shady_thinker_amd import model as M
+
+pytestmark = pytest.mark.gpu
+
+TOL_DECODE = 1e-4   # rel-L2, f32-accumulate matvec (north_star)
+TOL_GEMM = 2e-3     # rel-L2, f16-MFMA GEMM (north_star)
+
+
+def up(gpu, c, tiled=True):
+    return sta.GptqWeight.upload(gpu, c["qweight"], c["scales"], c["gs"], qzeros=c["qzeros"], g_idx=c["g_idx"],
+                                 tiled=tiled)
+
+
+def ref(orc, x, c):
+    return orc.gptq_matvec_f64(x, c["qweight"], c["scales"], c["K"], c["N"], c["gs"], qzeros=c["qzeros"],
+                               g_idx=c["g_idx"])
+
+
+@pytest.mark.parametrize("Mr,K,N,gs,zeros,act,tiled", [
+    (40, 512, 264, 128, True, True, True),
+    (200, 1024, 520, 64, False, False, True),
+    (33, 768, 136, 256, True, False, False),
+])
+def test_silu_gemm(gpu, orc, Mr, K, N, gs, zeros, act, tiled):
+    """C = (silu(g) * u) . dequant(W) for a block of tokens: the reference's
+    fused_silu_gptq_down, M rows at a time, against f64 (silu of the f16
+    inputs, then the f64 matvec); f16 and f32 outputs."""
+    c = orc.gptq_case(60 + gs, K, N, gs, zeros=zeros, act_order=act)
+    rng = np.random.default_rng(Mr)
+    g = rng.standard_normal((Mr, K)).astype(np.float16)
+    u = rng.standard_normal((Mr, K)).astype(np.float16)
+    w = up(gpu, c, tiled)
+    want = ref(orc, orc.silu_gate_f64(g, u), c)
+    for dt in (torch.float32, torch.float16):
+        y = torch.empty(Mr, N, device="cuda", dtype=dt)
+        M.fused_silu_gptq_gemm(gpu, torch.from_numpy(g).cuda(), torch.from_numpy(u).cuda(), w.qweight, w.scales, y,
+                               K, N, gs, w.qzeros, w.perm, w.flags)
+        torch.cuda.synchronize()
+        e = orc.rel_l2(y.float().cpu().numpy(), want)
+        print(f"silu GEMM M={Mr} K={K} N={N} gs={gs} {dt}: rel-L2 {e:.3e}")
+        assert e < TOL_GEMM
+
+
+def test_silu_gemm_zero_gate(gpu, orc):
+    """silu(0) = 0: a zero gate gives C = 0 exactly whatever up holds."""
+    K, N, Mr = 512, 72, 48
+    c = orc.gptq_case(61, K, N, 128)
+    w = up(gpu, c)
+    g = torch.zeros(Mr, K, device="cuda", dtype=torch.float16)
+    u = torch.randn(Mr, K, device="cuda").half()
+    y = torch.full((Mr, N), 7.0, device="cuda")
+    M.fused_silu_gptq_gemm(gpu, g, u, w.qweight, w.scales, y, K, N, 128, flags=w.flags)
+    torch.cuda.synchronize()
+    assert torch.count_nonzero(y).item() == 0
+
+
+def _layer(gpu, orc, H, Q, KV, I, gs, zeros=False):
+    cs = {}
+    for i, (name, k, n) in enumerate((("q", H, Q), ("k", H, KV), ("v", H, KV), ("o", Q, H), ("gate", H, I),
+                                       ("up", H, I), ("down", I, H))):
+        cs[name] = orc.gptq_case(300 + i, k, n, gs, zeros=zeros)
+    ws = {n: up(gpu, c) for n, c in cs.items()}
+    return cs, sta.DecoderLinears(ws["q"], ws["k"], ws["v"], ws["o"], ws["gate"], ws["up"], ws["down"])
+
+
+@pytest.mark.parametrize("Mr", [1, 3, 20])
+def test_decoder_linears_decode(gpu, orc, Mr):
+    """One layer's projections for 1-32 tokens (f32): q|k|v, o, h =
+    silu(x.Wg) * (x.Wu) and down on h, each against the f64 oracle."""
+    H, Q, KV, I, gs = 256, 256, 128, 512, 128
+    cs, layer = _layer(gpu, orc, H, Q, KV, I, gs, zeros=True)
+    rng = np.random.default_rng(Mr)
+    x = rng.standard_normal((Mr, H)).astype(np.float32)
+    attn = rng.standard_normal((Mr, Q)).astype(np.float32)
+    qkv = torch.empty(Mr, Q + 2 * KV, device="cuda")
+    o = torch.empty(Mr, H, device="cuda")
+    h = torch.empty(Mr, I, device="cuda")
+    d = torch.empty(Mr, H, device="cuda")
+    layer.decode(gpu, torch.from_numpy(x).cuda(), torch.from_numpy(attn).cuda(), qkv, o, h, d)
+    torch.cuda.synchronize()
+    want_qkv = np.concatenate([ref(orc, x, cs[n]) for n in ("q", "k", "v")], axis=1)
+    want_h = orc.silu_gate_f64(ref(orc, x, cs["gate"]), ref(orc, x, cs["up"]))
+    assert orc.rel_l2(qkv.cpu().numpy(), want_qkv) < TOL_DECODE
+    assert orc.rel_l2(o.cpu().numpy(), ref(orc, attn, cs["o"])) < TOL_DECODE
+    assert orc.rel_l2(h.cpu().numpy(), want_h) < TOL_DECODE
+    # down on the h this call produced (f32, as the reference's chain)
+    assert orc.rel_l2(d.cpu().numpy(), ref(orc, h.cpu().numpy(), cs["down"])) < TOL_DECODE
+
+
+def test_decoder_linears_prefill(gpu, orc):
+    """One layer's projections for a 48-token block (f16) through the GEMM:
+    q|k|v, o, gate, up, and down on silu(gate) * up fused into the GEMM's A
+    pass, each against the f64 oracle on the same f16 inputs."""
+    H, Q, KV, I, gs, Mr = 256, 256, 128, 512, 128, 48
+    cs, layer = _layer(gpu, orc, H, Q, KV, I, gs)
+    rng = np.random.default_rng(5)
+    x = rng.standard_normal((Mr, H)).astype(np.float16)
+    attn = rng.standard_normal((Mr, Q)).astype(np.float16)
+    f16 = dict(device="cuda", dtype=torch.float16)
+    qkv, o = torch.empty(Mr, Q + 2 * KV, **f16), torch.empty(Mr, H, **f16)
+    g, u, d = torch.empty(Mr, I, **f16), torch.empty(Mr, I, **f16), torch.empty(Mr, H, **f16)
+    layer.prefill(gpu, torch.from_numpy(x).cuda(), torch.from_numpy(attn).cuda(), qkv, o, g, u, d)
+    torch.cuda.synchronize()
+    want_qkv = np.concatenate([ref(orc, x, cs[n]) for n in ("q", "k", "v")], axis=1)
+    assert orc.rel_l2(qkv.float().cpu().numpy(), want_qkv) < TOL_GEMM
+    assert orc.rel_l2(o.float().cpu().numpy(), ref(orc, attn, cs["o"])) < TOL_GEMM
+    assert orc.rel_l2(g.float().cpu().numpy(), ref(orc, x, cs["gate"])) < TOL_GEMM
+    assert orc.rel_l2(u.float().cpu().numpy(), ref(orc, x, cs["up"])) < TOL_GEMM
+    want_d = ref(orc, orc.silu_gate_f64(g.cpu().numpy(), u.cpu().numpy()), cs["down"])
+    assert orc.rel_l2(d.float().cpu().numpy(), want_d) < TOL_GEMM
+
+
+def test_decoder_linears_shape_checks(gpu, orc):
+    cs, layer = _layer(gpu, orc, 256, 256, 128, 512, 128)
+    x = torch.zeros(40, 256, device="cuda")
+    with pytest.raises(ValueError):
+        layer.decode(gpu, x, torch.zeros(40, 256, device="cuda"), None, None, None, None)
+    w = {n: up(gpu, c) for n, c in cs.items()}
+    with pytest.raises(ValueError):
+        sta.DecoderLinears(w["q"], w["k"], w["v"], w["o"], w["gate"], w["up"], w["o"])
