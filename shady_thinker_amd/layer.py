@@ -45,6 +45,19 @@ class DecoderLinears:
         self.o, self.gate, self.up, self.down = o, gate, up, down
         self.hidden, self.attn_dim, self.inter = q.K, o.K, gate.N
 
+    @classmethod
+    def from_linears(cls, linears: dict, layer: int, layer_prefix: str = "model.layers") -> "DecoderLinears":
+        """A self-attention layer from load_gptq_checkpoint's {prefix:
+        GptqWeight}, by the tensor names the reference's loader takes:
+        {layer_prefix}.{i}.self_attn.{q,k,v,o}_proj (src/weights.rs:448-455)
+        and {layer_prefix}.{i}.mlp.{gate,up,down}_proj (:494-499)."""
+        pfx = f"{layer_prefix}.{layer}"
+        names = [f"{pfx}.self_attn.{p}_proj" for p in "qkvo"] + [f"{pfx}.mlp.{p}_proj" for p in ("gate", "up", "down")]
+        missing = [n for n in names if n not in linears]
+        if missing:
+            raise KeyError(f"DecoderLinears.from_linears: no GPTQ linear {missing[0]}")
+        return cls(*(linears[n] for n in names))
+
     def nbytes(self) -> int:
         return sum(w.nbytes for w in (self.qkv, self.o, self.gate, self.up, self.down))
 

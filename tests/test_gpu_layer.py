@@ -126,3 +126,31 @@ def test_decoder_linears_shape_checks(gpu, orc):
     w = {n: up(gpu, c) for n, c in cs.items()}
     with pytest.raises(ValueError):
         sta.DecoderLinears(w["q"], w["k"], w["v"], w["o"], w["gate"], w["up"], w["o"])
+
+
+def test_decoder_linears_from_checkpoint_names(gpu, orc):
+    """DecoderLinears.from_linears picks a layer's projections by the
+    reference loader's tensor names and computes what the direct
+    construction computes, bit for bit; a missing projection is a KeyError."""
+    H, Q, KV, I, gs, Mr = 256, 256, 128, 512, 128, 2
+    cs = {n: orc.gptq_case(400 + i, k, m, gs) for i, (n, k, m) in enumerate(
+        (("q", H, Q), ("k", H, KV), ("v", H, KV), ("o", Q, H), ("gate", H, I), ("up", H, I), ("down", I, H)))}
+    ws = {n: up(gpu, c) for n, c in cs.items()}
+    names = {"q": "self_attn.q_proj", "k": "self_attn.k_proj", "v": "self_attn.v_proj", "o": "self_attn.o_proj",
+             "gate": "mlp.gate_proj", "up": "mlp.up_proj", "down": "mlp.down_proj"}
+    linears = {f"model.layers.3.{names[n]}": w for n, w in ws.items()}
+    a = sta.DecoderLinears.from_linears(linears, 3)
+    b = sta.DecoderLinears(ws["q"], ws["k"], ws["v"], ws["o"], ws["gate"], ws["up"], ws["down"])
+    x = torch.randn(Mr, H, device="cuda")
+    attn = torch.randn(Mr, Q, device="cuda")
+    outs = []
+    for layer in (a, b):
+        bufs = [torch.empty(Mr, n, device="cuda") for n in (Q + 2 * KV, H, I, H)]
+        layer.decode(gpu, x, attn, *bufs)
+        torch.cuda.synchronize()
+        outs.append([t.cpu().numpy() for t in bufs])
+    for p_, q_ in zip(*outs):
+        assert np.array_equal(p_, q_)
+    del linears["model.layers.3.mlp.up_proj"]
+    with pytest.raises(KeyError):
+        sta.DecoderLinears.from_linears(linears, 3)
