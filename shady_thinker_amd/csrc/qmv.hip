@@ -69,7 +69,7 @@ __global__ __launch_bounds__(256) void repack8_kernel(const int8_t *__restrict__
 // The GPTQ entry points take the f16-MFMA kernel (tiled weights, no
 // act-order, f32 or f16 x) from this many tokens on, when N has more
 // 16-column tiles than the GPU has CUs (as measured on configs[4]'s shapes:
-// at 16 tokens q|k|v 12.1 -> 11.2 us, gate/up 20.2 -> 18.0, lm_head 134 -> 83;
+// at 16 tokens q|k|v 12.0 -> 10.7 us, gate/up 20.2 -> 17.4, lm_head 134 -> 75;
 // with fewer tiles or tokens the integer-limb kernels are faster).
 constexpr int kI4mmMinM = 12;
 
