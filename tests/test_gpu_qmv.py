@@ -836,3 +836,17 @@ def test_int4_mm_f16_graph_replay(gpu, orc, monkeypatch):
         g.replay()
         torch.cuda.synchronize()
         assert torch.equal(y, ye) and torch.equal(h, he)
+
+
+def test_int4_mm_f16_zeros_plus_one(gpu, orc, monkeypatch):
+    """AutoGPTQ-v1 zero points (stored z - 1, ST_FLAG_ZEROS_PLUS_ONE) on the
+    f16-MFMA kernel, matvec and gate/up, against the f64 oracle."""
+    _force_i4mm(monkeypatch)
+    Mr, K, N, gs = 14, 1280, 392, 128
+    c = orc.gptq_case(180, K, N, gs, zeros=True, M=Mr)
+    c2 = orc.gptq_case(181, K, N, gs, zeros=True)
+    w, w2 = up(gpu, c, zeros_plus_one=True), up(gpu, c2, zeros_plus_one=True)
+    g = orc.gptq_matvec_f64(c["x"], c["qweight"], c["scales"], K, N, gs, qzeros=c["qzeros"], zero_offset=1)
+    u = orc.gptq_matvec_f64(c["x"], c2["qweight"], c2["scales"], K, N, gs, qzeros=c2["qzeros"], zero_offset=1)
+    assert orc.rel_l2(run_matvec(gpu, w, c["x"]), g) < 1e-5
+    assert orc.rel_l2(_gate_up(gpu, w, w2, c["x"]), orc.silu_gate_f64(g, u)) < 1e-5
