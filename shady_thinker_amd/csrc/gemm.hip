@@ -279,6 +279,10 @@ __global__ __launch_bounds__(kThreads, kWavesPerSimd) void gemm_kernel(const _Fl
         load_groups(BUF ^ 1, kn);
         a_dma(std::integral_constant<int, BUF ^ 1>{}, kn);  // stage BUF ^ 1 was last read before the previous barrier
         load_b(bw[BUF ^ 1], kn);
+        // Keep the prefetch here: left alone, the scheduler sinks these loads
+        // to the end of the tile (shorter live ranges), where the barrier
+        // then waits for their whole latency.
+        __builtin_amdgcn_sched_barrier(0);
         half8 af[2][RB];
         auto read_a = [&](int t, int slot) {
 #pragma unroll
