@@ -51,6 +51,9 @@ constexpr int WN = 4;                // waves along N (1 along M)
 constexpr int RB = 4, CB = 2;        // 32 x 32 MFMA blocks per wave (rows, columns)
 constexpr int KT = 128;              // k per LDS tile
 constexpr int kThreads = 256;
+#ifndef ST_GEMM_VPM
+#define ST_GEMM_VPM 3  // VALU instructions scheduled after each MFMA
+#endif
 #ifndef ST_GEMM_WAVES
 #define ST_GEMM_WAVES 2
 #endif
@@ -283,30 +286,44 @@ __global__ __launch_bounds__(kThreads, kWavesPerSimd) void gemm_kernel(const _Fl
         // to the end of the tile (shorter live ranges), where the barrier
         // then waits for their whole latency.
         __builtin_amdgcn_sched_barrier(0);
-        half8 af[2][RB];
-        auto read_a = [&](int t, int slot) {
-#pragma unroll
-            for (int rb = 0; rb < RB; ++rb)
-            {
-                const int row = mw + rb * 32 + l32;
-                const _Float16 *as = BUF ? As1 : As0;
-                af[slot][rb] = *reinterpret_cast<const half8 *>(&as[row * KT + 8 * (kchunk(t) ^ (row & 15))]);
-            }
+        half8 af[RB];
+        auto read_a1 = [&](int t, int rb) {
+            const int row = mw + rb * 32 + l32;
+            const _Float16 *as = BUF ? As1 : As0;
+            af[rb] = *reinterpret_cast<const half8 *>(&as[row * KT + 8 * (kchunk(t) ^ (row & 15))]);
         };
-        read_a(0, 0);
+#pragma unroll
+        for (int rb = 0; rb < RB; ++rb) read_a1(0, rb);
+        // One A fragment per row block: it is reloaded for step t + 1 right
+        // after its last MFMA of step t. B of step t + 1 is converted while
+        // step t's MFMAs run. The scheduling groups interleave them (one
+        // MFMA, then a share of the VALU and LDS reads), so that one wave
+        // keeps the matrix and vector units busy together.
+        half8 bf[2][CB];
+        if ((BUF * KT) % GS == 0) group_consts(BUF, 0);
+#pragma unroll
+        for (int cb = 0; cb < CB; ++cb) bf[0][cb] = word_to_b(bw[BUF][0][cb], bc[cb]);
 #pragma unroll
         for (int t = 0; t < KT / 16; ++t) {
             const int cur = t & 1;
-            if (t + 1 < KT / 16) read_a(t + 1, cur ^ 1);
-            if ((BUF * KT + 16 * t) % GS == 0) group_consts(BUF, (16 * t) / GS);
-            half8 bf[CB];
 #pragma unroll
-            for (int cb = 0; cb < CB; ++cb) bf[cb] = word_to_b(bw[BUF][t][cb], bc[cb]);
-#pragma unroll
-            for (int rb = 0; rb < RB; ++rb)
+            for (int rb = 0; rb < RB; ++rb) {
 #pragma unroll
                 for (int cb = 0; cb < CB; ++cb)
-                    acc[rb][cb] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af[cur][rb], bf[cb], acc[rb][cb], 0, 0, 0);
+                    acc[rb][cb] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af[rb], bf[cur][cb], acc[rb][cb], 0, 0, 0);
+                if (t + 1 < KT / 16) read_a1(t + 1, rb);
+            }
+            if (t + 1 < KT / 16) {
+                if ((BUF * KT + 16 * (t + 1)) % GS == 0) group_consts(BUF, (16 * (t + 1)) / GS);
+#pragma unroll
+                for (int cb = 0; cb < CB; ++cb) bf[cur ^ 1][cb] = word_to_b(bw[BUF][t + 1][cb], bc[cb]);
+#pragma unroll
+                for (int i = 0; i < RB * CB; ++i) {
+                    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);                   // one MFMA
+                    if (i % CB == CB - 1) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // its row block's next A
+                    __builtin_amdgcn_sched_group_barrier(0x002, ST_GEMM_VPM, 0);         // VALU
+                }
+            }
         }
         __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): next tile's A DMAs (and B words) landed
         __syncthreads();
