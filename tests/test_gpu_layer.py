@@ -154,3 +154,46 @@ def test_decoder_linears_from_checkpoint_names(gpu, orc):
     del linears["model.layers.3.mlp.up_proj"]
     with pytest.raises(KeyError):
         sta.DecoderLinears.from_linears(linears, 3)
+
+
+def test_gemm_argument_errors(gpu, orc):
+    """The prefill entry points reject bad arguments with a status (the
+    reference panics there) and launch nothing: NULL operands, a group size
+    outside {64, 128, 256}, K not a multiple of 128, N not a multiple of 8,
+    an output dtype other than f32/f16, misaligned A."""
+    from shady_thinker_amd import _lib as L
+    from shady_thinker_amd.gpu import ptr as p
+    INVALID, SHAPE, ALIGN = 1, 2, 3  # st_status (include/shady_hip.h)
+    K, N, Mr = 256, 64, 8
+    c = orc.gptq_case(62, K, N, 128)
+    w = up(gpu, c)
+    a = torch.randn(Mr, K, device="cuda").half()
+    u = torch.randn(Mr, K, device="cuda").half()
+    y = torch.full((Mr, N), 3.0, device="cuda")
+    gpu.sync_stream()
+
+    def gemm(a_, k=K, n=N, gs=128, dt=L.ST_F32):
+        L.call("st_gptq_i4_gemm", gpu.handle, a_, p(w.qweight), p(w.scales), None, None, p(y), dt, Mr, k, n, gs,
+               w.flags)
+
+    def silu(g_, u_, k=K, n=N, gs=128, dt=L.ST_F32):
+        L.call("st_gptq_i4_silu_gemm", gpu.handle, g_, u_, p(w.qweight), p(w.scales), None, None, p(y), dt, Mr, k,
+               n, gs, w.flags)
+
+    cases = [
+        (lambda: gemm(None), INVALID),
+        (lambda: gemm(p(a), gs=32), SHAPE),
+        (lambda: gemm(p(a), k=200), SHAPE),
+        (lambda: gemm(p(a), n=60), SHAPE),
+        (lambda: gemm(p(a), dt=L.ST_BF16), INVALID),
+        (lambda: gemm(p(a) + 2), ALIGN),
+        (lambda: silu(p(a), None), INVALID),
+        (lambda: silu(None, p(u)), INVALID),
+        (lambda: silu(p(a), p(u), gs=512), SHAPE),
+    ]
+    for fn, code in cases:
+        with pytest.raises(L.ShadyHipError) as ei:
+            fn()
+        assert ei.value.code == code, str(ei.value)
+    torch.cuda.synchronize()
+    assert bool((y == 3.0).all())  # nothing was written
