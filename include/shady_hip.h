@@ -89,6 +89,32 @@ int st_context_reserve_workspace(st_context *ctx, size_t bytes);
 
 int st_context_destroy(st_context *ctx);
 
+/* Kernel-path overrides of one context. No counterpart in the reference (its
+ * WGSL path has one shader per op); for tests that force each path and for
+ * tuning. Every setting starts at -1 (automatic: the library's shape rules
+ * choose); a call made after a change uses the new value. Nothing is read
+ * from the environment. */
+typedef enum {
+    ST_TUNE_DECODE_KERNEL = 0, /* 1-4 tokens on tiled weights: 0 register-ring, 1 streaming */
+    ST_TUNE_STAGE_MODE,        /* register-ring, one token block: 1 staging waves, 2 per-wave staging */
+    ST_TUNE_STAGE_ROUNDS,      /* register-ring staging waves: 64-item rounds each (1..4) */
+    ST_TUNE_WAVES,             /* register-ring, one tile per workgroup: waves (4..16) */
+    ST_TUNE_NO_COOP,           /* 1: register-ring per-wave fallback only */
+    ST_TUNE_ONE_TILE,          /* 1: one 16-column tile per workgroup */
+    ST_TUNE_NO_CHUNK,          /* 1: no K-chunked cooperative staging (several tokens) */
+    ST_TUNE_NO_KSPLIT,         /* 1: no split-K of several-token decode on few tiles */
+    ST_TUNE_SPLIT_TILES_CU,    /* several-token decode: split K up to this many tiles per CU */
+    ST_TUNE_TOKEN_BLOCK,       /* decode: tokens per launch (1..16) */
+    ST_TUNE_I4MM_MIN_M,        /* GPTQ decode: fewest tokens for the f16-MFMA kernel */
+    ST_TUNE_I4MM_MIN_TILES,    /* GPTQ decode: fewest 16-column tiles for the f16-MFMA kernel */
+    ST_TUNE_I8MM_MIN_M,        /* INT8 decode: fewest tokens for the f16-MFMA kernel */
+    ST_TUNE_GEMM_CB,           /* prefill GEMM: 32-column blocks per wave (1 or 2) */
+    ST_TUNE_GEMM_NO_SPLIT,     /* 1: prefill GEMM without split-K */
+    ST_TUNE_COUNT
+} st_tune;
+int st_context_set_tune(st_context *ctx, int knob, int value);
+int st_context_get_tune(st_context *ctx, int knob, int *value);
+
 /* Replaces GpuContext::create_buffer / create_storage_buffer (src/gpu.rs:80-103): device
  * allocation, size rounded up to 4 bytes, 256-byte aligned. */
 int st_alloc(st_context *ctx, size_t bytes, void **out);

@@ -19,6 +19,11 @@ ST_F32, ST_F16, ST_BF16 = 0, 1, 2
 ST_FLAG_ZEROS_PLUS_ONE = 0x1
 ST_FLAG_TILED = 0x2
 
+# st_tune (include/shady_hip.h): kernel-path overrides of one context
+TUNE_KNOBS = ("DECODE_KERNEL", "STAGE_MODE", "STAGE_ROUNDS", "WAVES", "NO_COOP", "ONE_TILE", "NO_CHUNK", "NO_KSPLIT",
+              "SPLIT_TILES_CU", "TOKEN_BLOCK", "I4MM_MIN_M", "I4MM_MIN_TILES", "I8MM_MIN_M", "GEMM_CB", "GEMM_NO_SPLIT")
+TUNE = {name: i for i, name in enumerate(TUNE_KNOBS)}
+
 STATUS_NAMES = {
     0: "ST_OK", 1: "ST_ERR_INVALID", 2: "ST_ERR_SHAPE", 3: "ST_ERR_ALIGN",
     4: "ST_ERR_UNSUPPORTED", 5: "ST_ERR_HIP", 6: "ST_ERR_WORKSPACE", 7: "ST_ERR_OOM",
@@ -48,6 +53,8 @@ _SIGNATURES = {
     "st_context_stream": (_P, [_P]),
     "st_context_reserve_workspace": (_I, [_P, _SZ]),
     "st_context_destroy": (_I, [_P]),
+    "st_context_set_tune": (_I, [_P, _I, _I]),
+    "st_context_get_tune": (_I, [_P, _I, ctypes.POINTER(_I)]),
     "st_alloc": (_I, [_P, _SZ, ctypes.POINTER(_P)]),
     "st_free": (_I, [_P, _P]),
     "st_upload": (_I, [_P, _P, _P, _SZ]),

@@ -21,9 +21,20 @@ struct st_context {
     // what it uses; calls on one context are ordered by its stream).
     float *ws = nullptr;
     size_t ws_bytes = 0;
+    // kernel-path overrides (st_tune); -1 = automatic
+    int tune[ST_TUNE_COUNT];
+    st_context() {
+        for (int &t : tune) t = -1;
+    }
 };
 
 namespace st {
+
+// A kernel-path setting of the context, or `dflt` when it is automatic.
+inline int tune(const st_context *ctx, int knob, int dflt) {
+    const int v = ctx->tune[knob];
+    return v < 0 ? dflt : v;
+}
 
 void set_error(const char *fmt, ...);
 void clear_error();

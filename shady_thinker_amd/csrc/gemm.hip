@@ -487,10 +487,10 @@ int launch_tiled(st_context *ctx, const _Float16 *A, const uint32_t *qw, const u
 
 // 32-column blocks per wave: 1 (128 x 128 tiles) when 128 x 256 tiles would
 // give at most one workgroup per CU (then two waves per SIMD instead of
-// one); ST_GEMM_CB forces 1 or 2.
+// one); ST_TUNE_GEMM_CB forces 1 or 2.
 int pick_cb(st_context *ctx, int M, int N) {
-    const char *e = std::getenv("ST_GEMM_CB");
-    if (e && (*e == '1' || *e == '2')) return *e - '0';
+    const int f = st::tune(ctx, ST_TUNE_GEMM_CB, 0);
+    if (f == 1 || f == 2) return f;
     const int T2 = ((M + BM - 1) / BM) * ((N + BN - 1) / BN);
     return T2 <= ctx->num_cus ? 1 : 2;
 }
@@ -505,8 +505,7 @@ Split plan_split(st_context *ctx, int M, int K, int N, int cb, size_t ws_used) {
     const int T = ((M + BM - 1) / BM) * ((N + 32 * cb * WN - 1) / (32 * cb * WN));
     const int slots = 2 * ctx->num_cus;
     const int ntiles = K / KT;
-    const char *no_split = std::getenv("ST_GEMM_NO_SPLIT");
-    if (2 * T > ctx->num_cus || ntiles < 8 || (no_split && *no_split && *no_split != '0')) return sp;
+    if (2 * T > ctx->num_cus || ntiles < 8 || st::tune(ctx, ST_TUNE_GEMM_NO_SPLIT, 0)) return sp;
     int S = std::min({8, (slots + T - 1) / T, ntiles / 4});
     const size_t off = (ws_used + 255) & ~size_t(255);
     while (S > 1 && off + (size_t)S * M * N * sizeof(float) > ctx->ws_bytes) --S;

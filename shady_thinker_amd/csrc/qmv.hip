@@ -75,8 +75,8 @@ constexpr int kI4mmMinM = 12;
 
 bool use_i4mm(const st_context *ctx, const QmvParams &p, bool tiled, int xm) {
     const int ntiles = (p.N + kTileN - 1) / kTileN;
-    const int min_m = std::max(2, st::qmv::env_int("ST_I4MM_MIN_M", kI4mmMinM));
-    const int min_tiles = st::qmv::env_int("ST_I4MM_MIN_TILES", ctx->num_cus + 1);
+    const int min_m = std::max(2, st::tune(ctx, ST_TUNE_I4MM_MIN_M, kI4mmMinM));
+    const int min_tiles = st::tune(ctx, ST_TUNE_I4MM_MIN_TILES, ctx->num_cus + 1);
     return tiled && !p.perm && (xm == XM_F32 || xm == XM_F16) && p.M <= 16 && p.M >= min_m && ntiles >= min_tiles &&
            p.K % 128 == 0 && (size_t)ntiles * kTileN * p.K / 2 < (size_t(1) << 31);
 }
@@ -105,8 +105,8 @@ constexpr int kTokenBlock = 16;
 constexpr int kI8mmMinM = 2;
 
 template <typename F>
-int by_token_blocks(QmvParams &p, int xm, F &&launch) {
-    const int blk = std::max(1, std::min(kTokenBlock, st::qmv::env_int("ST_QMV_BLOCK", kTokenBlock)));
+int by_token_blocks(const st_context *ctx, QmvParams &p, int xm, F &&launch) {
+    const int blk = std::max(1, std::min(kTokenBlock, st::tune(ctx, ST_TUNE_TOKEN_BLOCK, kTokenBlock)));
     if (p.M <= blk) return launch(p);
     const size_t xe = xm == XM_F16 ? 2 : 4;
     for (int m0 = 0; m0 < p.M; m0 += blk) {
@@ -157,7 +157,7 @@ int st_gptq_i4_matvec(st_context *ctx, const void *x, int x_dtype, const uint32_
     p.zoff = (flags & ST_FLAG_ZEROS_PLUS_ONE) ? 1 : 0;
     const bool tiled = flags & ST_FLAG_TILED;
     const int xm = x_dtype == ST_F32 ? XM_F32 : XM_F16;
-    return by_token_blocks(p, xm, [&](QmvParams &q) { return launch_i4(ctx, q, tiled, 1, xm); });
+    return by_token_blocks(ctx, p, xm, [&](QmvParams &q) { return launch_i4(ctx, q, tiled, 1, xm); });
 }
 
 int st_gptq_i4_silu_matvec(st_context *ctx, const float *a, const float *b, const uint32_t *qweight,
@@ -182,7 +182,7 @@ int st_gptq_i4_silu_matvec(st_context *ctx, const float *a, const float *b, cons
     p.gs = group_size;
     p.zoff = (flags & ST_FLAG_ZEROS_PLUS_ONE) ? 1 : 0;
     const bool tiled = flags & ST_FLAG_TILED;
-    return by_token_blocks(p, XM_SILU, [&](QmvParams &q) { return launch_i4(ctx, q, tiled, 1, XM_SILU); });
+    return by_token_blocks(ctx, p, XM_SILU, [&](QmvParams &q) { return launch_i4(ctx, q, tiled, 1, XM_SILU); });
 }
 
 int st_gptq_i4_gate_up_silu(st_context *ctx, const void *x, int x_dtype, const uint32_t *qweight_gate,
@@ -216,7 +216,7 @@ int st_gptq_i4_gate_up_silu(st_context *ctx, const void *x, int x_dtype, const u
     p.zoff = (flags & ST_FLAG_ZEROS_PLUS_ONE) ? 1 : 0;
     const bool tiled = flags & ST_FLAG_TILED;
     const int xm = x_dtype == ST_F32 ? XM_F32 : XM_F16;
-    return by_token_blocks(p, xm, [&](QmvParams &q) { return launch_i4(ctx, q, tiled, 2, xm); });
+    return by_token_blocks(ctx, p, xm, [&](QmvParams &q) { return launch_i4(ctx, q, tiled, 2, xm); });
 }
 
 size_t st_gptq_i4_tiled_words(int K, int N, int group_size) {
@@ -268,7 +268,7 @@ int st_int8_matvec(st_context *ctx, const void *x, int x_dtype, const int8_t *w,
     if (x_dtype != ST_F32 && x_dtype != ST_F16) return st::fail(ST_ERR_INVALID, "st_int8_matvec: x_dtype %d", x_dtype);
     // Several tokens with f16 x on tiled weights: the f16-MFMA skinny GEMM,
     // which reads the weights once for all tokens.
-    if (tiled && x_dtype == ST_F16 && M >= st::qmv::env_int("ST_I8MM_MIN_M", kI8mmMinM))
+    if (tiled && x_dtype == ST_F16 && M >= st::tune(ctx, ST_TUNE_I8MM_MIN_M, kI8mmMinM))
         return st::int8_mm_f16(ctx, x, w, scale, y, M, K, N);
     QmvParams p{};
     p.x = x;
@@ -282,7 +282,7 @@ int st_int8_matvec(st_context *ctx, const void *x, int x_dtype, const int8_t *w,
     p.units = K / 128;
     p.ntiles = (N + kTileN - 1) / kTileN;
     const int xm = x_dtype == ST_F32 ? XM_F32 : XM_F16;
-    return by_token_blocks(p, xm, [&](QmvParams &q) {
+    return by_token_blocks(ctx, p, xm, [&](QmvParams &q) {
         return tiled ? dispatch<FMT_I8T, false>(ctx, q, 1, xm) : dispatch<FMT_I8, false>(ctx, q, 1, xm);
     });
 }

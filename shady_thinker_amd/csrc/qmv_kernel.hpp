@@ -230,6 +230,80 @@ __device__ __forceinline__ unsigned pack4(unsigned a, unsigned b, unsigned c, un
     return __builtin_amdgcn_perm(hi, lo, 0x05040100u);
 }
 
+// One staging item: 16 values of x (token m, k0 .. k0+15 of a group,
+// already converted to f32) become three signed 8-bit limbs per value,
+// written as the A-operand rows dst[0..2] (dst[3], the token's fourth row, is
+// zero), with the group's scale 2^-e and the split of sum(X) into es_dst
+// when the item is the group's first (es_dst non-null). The IPU lanes of a
+// group are consecutive and aligned; every lane calls (the cross-lane max and
+// sum need them all), `ok` = the item exists. NAT: operand byte J holds value
+// J (INT8), else value i4_koff(J) (GPTQ nibble order).
+template <int IPU, bool NAT>
+__device__ __forceinline__ void quantize_item(float (&v)[16], bool ok, u32x4 *dst, u32x4 *es_dst) {
+    float amax = 0.0f, nf = 0.0f;
+#pragma unroll
+    for (int j = 0; j < 16; ++j) {
+        amax = fmaxf(amax, fabsf(v[j]));
+        nf = fmaf(v[j], 0.0f, nf);  // NaN iff some x is NaN or inf
+    }
+    // a non-finite x poisons its group: amax = inf -> 2^-e = NaN -> y = NaN
+    amax = (nf == nf) ? amax : INFINITY;
+    if (!ok) amax = 0.0f;
+    amax = group_max<IPU>(amax);
+    int e = 0;
+    float em = 1.0f;
+    if (amax == INFINITY) {
+        em = __builtin_nanf("");
+    } else if (amax > 0.0f) {
+        // amax = f 2^fe, f in [0.5, 1): floor(log2 amax) = fe - 1
+        e = 22 - __builtin_amdgcn_frexp_expf(amax);
+        e = e > 100 ? 100 : (e < -100 ? -100 : e);
+        em = __builtin_amdgcn_ldexpf(1.0f, -e);
+    }
+    const float sc2 = __builtin_amdgcn_ldexpf(1.0f, e);
+    // X = round(x 2^e) in one FMA: |x 2^e| < 2^22 when amax is finite
+    // (otherwise the group is NaN anyway), so v = x 2^e + 1.5 * 2^23 lies in
+    // [2^23, 2^24), where the floats are the integers: the FMA rounds x 2^e
+    // to the nearest integer (ties to even) and bits(v) = 0x4B400000 + X.
+    unsigned Z[16];
+    unsigned ysum = 0;
+#pragma unroll
+    for (int j = 0; j < 16; ++j) {
+        const unsigned y = __builtin_bit_cast(unsigned, fmaf(v[j], sc2, 12582912.0f));
+        ysum += y;
+        // Z = Y + 0xC08080 = X + 0x8080 (mod 2^24): byte 2 of Z is the limb
+        // L2 = byte 2 of X + 32896, bytes 1 and 0 of Z are L1 = byte 1 of X +
+        // 128 and L0 = byte 0 of X, each plus 128 (mod 256)
+        Z[j] = y + 0xC08080u;
+    }
+    const int sum = group_sum<IPU>((int)(ysum - 16u * 0x4B400000u));
+    if (!ok) return;
+    u32x4 L2v, L1v, L0v;
+#pragma unroll
+    for (int rr = 0; rr < 4; ++rr) {
+        const unsigned a = Z[NAT ? 4 * rr : i4_koff(4 * rr)];
+        const unsigned bb = Z[NAT ? 4 * rr + 1 : i4_koff(4 * rr + 1)];
+        const unsigned cc = Z[NAT ? 4 * rr + 2 : i4_koff(4 * rr + 2)];
+        const unsigned dd = Z[NAT ? 4 * rr + 3 : i4_koff(4 * rr + 3)];
+        // [a0 b0 a1 b1], [c0 d0 c1 d1], [a2 b2 -- --], [c2 d2 -- --]
+        const unsigned ab01 = __builtin_amdgcn_perm(bb, a, 0x05010400u);
+        const unsigned cd01 = __builtin_amdgcn_perm(dd, cc, 0x05010400u);
+        const unsigned ab2 = __builtin_amdgcn_perm(bb, a, 0x0C0C0602u);
+        const unsigned cd2 = __builtin_amdgcn_perm(dd, cc, 0x0C0C0602u);
+        L2v[rr] = __builtin_amdgcn_perm(cd2, ab2, 0x05040100u);
+        L1v[rr] = __builtin_amdgcn_perm(cd01, ab01, 0x07060302u) ^ 0x80808080u;
+        L0v[rr] = __builtin_amdgcn_perm(cd01, ab01, 0x05040100u) ^ 0x80808080u;
+    }
+    dst[0] = L2v;
+    dst[1] = L1v;
+    dst[2] = L0v;
+    dst[3] = u32x4{0, 0, 0, 0};  // row 4t+3
+    if (es_dst) {
+        const int h = (sum + 32768) >> 16;
+        *es_dst = u32x4{__builtin_bit_cast(unsigned, em), (unsigned)(-h), (unsigned)(-(sum - (h << 16))), 0u};
+    }
+}
+
 // s_waitcnt vmcnt(0) (expcnt and lgkmcnt left at their maxima).
 __device__ __forceinline__ void wait_vm_all() { __builtin_amdgcn_s_waitcnt(0x0F70); }
 
@@ -503,75 +577,10 @@ __global__ __launch_bounds__((64 * (CM == 3 ? kChunkWaves<NSRC, MB> : kMaxWavesF
             const int ua = (COOP && !CHK) ? cs + ui : ui;  // A-region unit (COOP: the group itself)
             const bool ok = i < items && cs + ui < uend;
             x_finish<XM, PERM>(xv[r], xb[XM == XM_SILU ? r : 0]);
-            float amax = 0.0f, nf = 0.0f;
-#pragma unroll
-            for (int j = 0; j < 16; ++j) {
-                amax = fmaxf(amax, fabsf(xv[r][j]));
-                nf = fmaf(xv[r][j], 0.0f, nf);  // NaN iff some x is NaN or inf
-            }
-            // a non-finite x poisons its group: amax = inf -> 2^-e = NaN -> y = NaN
-            amax = (nf == nf) ? amax : INFINITY;
-            if (!ok) amax = 0.0f;
-            amax = group_max<IPU>(amax);
-            int e = 0;
-            float em = 1.0f;
-            if (amax == INFINITY) {
-                em = __builtin_nanf("");
-            } else if (amax > 0.0f) {
-                // amax = f 2^fe, f in [0.5, 1): floor(log2 amax) = fe - 1
-                e = 22 - __builtin_amdgcn_frexp_expf(amax);
-                e = e > 100 ? 100 : (e < -100 ? -100 : e);
-                em = __builtin_amdgcn_ldexpf(1.0f, -e);
-            }
-            const float sc2 = __builtin_amdgcn_ldexpf(1.0f, e);
-            // X = round(x 2^e) in one FMA: |x 2^e| < 2^22 when amax is finite
-            // (otherwise the group is NaN anyway), so v = x 2^e + 1.5 * 2^23
-            // lies in [2^23, 2^24), where the floats are the integers: the FMA
-            // rounds x 2^e to the nearest integer (ties to even) and bits(v) =
-            // 0x4B400000 + X.
-            unsigned Z[16];
-            unsigned ysum = 0;
-#pragma unroll
-            for (int j = 0; j < 16; ++j) {
-                const unsigned y = __builtin_bit_cast(unsigned, fmaf(xv[r][j], sc2, 12582912.0f));
-                ysum += y;
-                // Z = Y + 0xC08080 = X + 0x8080 (mod 2^24): byte 2 of Z is the
-                // limb L2 = byte 2 of X + 32896, bytes 1 and 0 of Z are L1 =
-                // byte 1 of X + 128 and L0 = byte 0 of X, each plus 128 (mod 256)
-                Z[j] = y + 0xC08080u;
-            }
-            int sum = group_sum<IPU>((int)(ysum - 16u * 0x4B400000u));
-            if (ok) {
-                // Operand byte J holds element koff(J) (GPTQ nibble order) or J.
-                u32x4 L2v, L1v, L0v;
-#pragma unroll
-                for (int rr = 0; rr < 4; ++rr) {
-                    constexpr bool nat = is_i8(FMT);
-                    const unsigned a = Z[nat ? 4 * rr : i4_koff(4 * rr)];
-                    const unsigned bb = Z[nat ? 4 * rr + 1 : i4_koff(4 * rr + 1)];
-                    const unsigned cc = Z[nat ? 4 * rr + 2 : i4_koff(4 * rr + 2)];
-                    const unsigned dd = Z[nat ? 4 * rr + 3 : i4_koff(4 * rr + 3)];
-                    // [a0 b0 a1 b1], [c0 d0 c1 d1], [a2 b2 -- --], [c2 d2 -- --]
-                    const unsigned ab01 = __builtin_amdgcn_perm(bb, a, 0x05010400u);
-                    const unsigned cd01 = __builtin_amdgcn_perm(dd, cc, 0x05010400u);
-                    const unsigned ab2 = __builtin_amdgcn_perm(bb, a, 0x0C0C0602u);
-                    const unsigned cd2 = __builtin_amdgcn_perm(dd, cc, 0x0C0C0602u);
-                    L2v[rr] = __builtin_amdgcn_perm(cd2, ab2, 0x05040100u);
-                    L1v[rr] = __builtin_amdgcn_perm(cd01, ab01, 0x07060302u) ^ 0x80808080u;
-                    L0v[rr] = __builtin_amdgcn_perm(cd01, ab01, 0x05040100u) ^ 0x80808080u;
-                }
-                const int st = ii >> 2, qq = ii & 3;
-                u32x4 *dst = abuf + (((size_t)(ua * SPU + st) * MB + (m >> 2)) * 4 + qq) * RB + 4 * (m & 3);
-                dst[0] = L2v;
-                dst[1] = L1v;
-                dst[2] = L0v;
-                dst[3] = u32x4{0, 0, 0, 0};  // row 4t+3 (see the zero fill below)
-                if (ii == 0) {
-                    const int h = (sum + 32768) >> 16;
-                    s_es[ua * M + m] = u32x4{__builtin_bit_cast(unsigned, em), (unsigned)(-h),
-                                             (unsigned)(-(sum - (h << 16))), 0u};
-                }
-            }
+            const int st = ii >> 2, qq = ii & 3;
+            quantize_item<IPU, is_i8(FMT)>(xv[r], ok,
+                                           abuf + (((size_t)(ua * SPU + st) * MB + (m >> 2)) * 4 + qq) * RB + 4 * (m & 3),
+                                           ii == 0 ? &s_es[ua * M + m] : nullptr);
         }
     };
 
@@ -861,11 +870,6 @@ __global__ __launch_bounds__(256) void split_reduce_kernel(const float *__restri
 
 // ----------------------------------------------------------------- host side
 
-inline int env_int(const char *name, int dflt) {
-    const char *v = std::getenv(name);
-    return (v && *v) ? std::atoi(v) : dflt;
-}
-
 // MFMA token blocks of 4 per launch (calls run in blocks of at most 16 tokens)
 inline int mb_for(int M) { return M <= 4 ? 1 : (M <= 8 ? 2 : 4); }
 
@@ -911,11 +915,11 @@ int launch_t(st_context *ctx, Params &p) {
         // (measured, configs[4] shapes: one token block splits only a long K,
         // down 17 -> 9.8 us at 4 tokens while o_proj, K = 4096, lost; four
         // blocks split up to 2 tiles per CU, qkv 18.4 -> 16.7 us at 16)
-        const int split_max = env_int("ST_QMV_SPLIT_TILES_CU", MB >= 4 ? 2 : kSplitTilesPerCu);
+        const int split_max = tune(ctx, ST_TUNE_SPLIT_TILES_CU, MB >= 4 ? 2 : kSplitTilesPerCu);
         const bool split = tiles_cu <= split_max && (MB > 1 || p.units >= kSplitMinUnits1);
         // (one token: the split's reduce launch costs more than it saves,
         // configs[4] down 7.2 -> 9.2 us)
-        if (p.M > 1 && (MB > 1 || split) && !env_int("ST_QMV_NO_CHUNK", 0)) {
+        if (p.M > 1 && (MB > 1 || split) && !tune(ctx, ST_TUNE_NO_CHUNK, 0)) {
             int grid, tpw, ks = 1;
             if (!split) {
                 grid = tiles_cu <= kMaxTilesPerWg ? ncu : (p.ntiles + kMaxTilesPerWg - 1) / kMaxTilesPerWg;
@@ -928,7 +932,7 @@ int launch_t(st_context *ctx, Params &p) {
                 tpw = std::min(kSplitTiles, p.ntiles);
                 grid = (p.ntiles + tpw - 1) / tpw;
                 ks = std::max(1, std::min({ncu / grid, kMaxKSplit, p.units / 2}));
-                if (env_int("ST_QMV_NO_KSPLIT", 0)) ks = 1;
+                if (tune(ctx, ST_TUNE_NO_KSPLIT, 0)) ks = 1;
                 const size_t need = (size_t)ks * NSRC * p.M * p.N * sizeof(float);
                 if (ks > 1 && (need > ctx->ws_bytes || !ctx->ws)) ks = 1;
             }
@@ -983,9 +987,9 @@ int launch_t(st_context *ctx, Params &p) {
             // owns several tiles (more waves left for K). When they would
             // take 6 or more waves (long K) or stage the costly silu(a)*b,
             // each wave stages its own groups instead (mode 2): all waves
-            // stream weights. ST_QMV_STAGE_MODE / _ROUNDS override (tuning).
-            const int mode = env_int("ST_QMV_STAGE_MODE", 0);
-            const int env_r = env_int("ST_QMV_STAGE_ROUNDS", 0);
+            // stream weights. ST_TUNE_STAGE_MODE / _ROUNDS override (tests, tuning).
+            const int mode = tune(ctx, ST_TUNE_STAGE_MODE, 0);
+            const int env_r = tune(ctx, ST_TUNE_STAGE_ROUNDS, 0);
             constexpr int CR = coop_rounds<XM>;
             const int r0 = env_r > 0 ? std::min(env_r, CR) : std::min(CR, tpw > 1 ? 2 : 1);
             const long long ns0 = (items + 64 * r0 - 1) / (64 * r0);
@@ -1009,10 +1013,10 @@ int launch_t(st_context *ctx, Params &p) {
             p.nstage = 0;
             return launch_kernel<FMT, NSRC, XM, MB, SPU, PERM, 2>(ctx, p, lds);
         };
-        if (!env_int("ST_QMV_NO_COOP", 0)) {
+        if (!tune(ctx, ST_TUNE_NO_COOP, 0)) {
             const int ncu = std::max(1, ctx->num_cus);
             const int tiles_cu = (p.ntiles + ncu - 1) / ncu;
-            if (tiles_cu >= 2 && !env_int("ST_QMV_ONE_TILE", 0)) {
+            if (tiles_cu >= 2 && !tune(ctx, ST_TUNE_ONE_TILE, 0)) {
                 // more tiles than CUs: a workgroup per CU (all the waves a CU
                 // holds) owns 2..kMaxTilesPerWg tiles and stages x once for them
                 // (every CU: a grid of ceil(ntiles / 3) even workgroups for
@@ -1025,7 +1029,7 @@ int launch_t(st_context *ctx, Params &p) {
             }
             int nw = want >= 16 ? 16 : (want >= 8 ? 8 : 4);
             nw = std::max(4, std::min({nw, NWX, std::max(4, p.units)}));
-            nw = std::max(4, std::min(NWX, env_int("ST_QMV_WAVES", nw)));
+            nw = std::max(4, std::min(NWX, tune(ctx, ST_TUNE_WAVES, nw)));
             // more waves when the staging waves leave too few for K (GPTQ:
             // at most kScaleUnits groups per wave, the scale block)
             for (;; nw = std::min(2 * nw, NWX)) {
@@ -1085,19 +1089,59 @@ int launch_gs(st_context *ctx, Params &p) {
 template <int FMT, bool PERM>
 int dispatch(st_context *ctx, Params &p, int nsrc, int xm);
 
+}  // namespace qmv
+}  // namespace st
+
+#include "qmv_stream.hpp"
+
+namespace st {
+namespace qmv {
+
+// 1-4 tokens on tiled weights: the streaming kernel (qmv_stream.hpp) from
+// this many 16-column tiles per CU on (graph replay, one token: the int4
+// lm_head 2560 x 151936, 37 tiles per CU, 50.7 -> 42.9 us, and 62.5 -> 43.6
+// us at 4 tokens; at 2-3 tiles per CU it ties (Llama-7B gate/up) or loses
+// (configs[4] gate/up 9.0 -> 9.9 us), and with one tile per CU or fewer the
+// register-ring kernel is 1.5-3 us faster).
+constexpr int kStreamMinTilesCu = 8;
+
+// The streaming kernel when it is chosen and the call fits it, else the
+// register-ring kernels.
+template <int FMT, int NSRC, int XM, bool PERM>
+int launch_fmt(st_context *ctx, Params &p) {
+    if constexpr (FMT == FMT_I4T || FMT == FMT_I8T) {
+        const int ncu = std::max(1, ctx->num_cus);
+        const int pick = tune(ctx, ST_TUNE_DECODE_KERNEL, -1);
+        if (p.M <= 4 && (pick == 1 || (pick < 0 && (p.ntiles + ncu - 1) / ncu >= kStreamMinTilesCu))) {
+            int rc = -1;
+            if constexpr (is_i8(FMT)) {
+                rc = launch_stream<FMT, NSRC, XM, 2, PERM>(ctx, p);
+            } else {
+                switch (p.gs) {
+                    case 64: rc = launch_stream<FMT, NSRC, XM, 1, PERM>(ctx, p); break;
+                    case 128: rc = launch_stream<FMT, NSRC, XM, 2, PERM>(ctx, p); break;
+                    case 256: rc = launch_stream<FMT, NSRC, XM, 4, PERM>(ctx, p); break;
+                }
+            }
+            if (rc != -1) return rc;
+        }
+    }
+    return launch_gs<FMT, NSRC, XM, PERM>(ctx, p);
+}
+
 template <int FMT, bool PERM>
 int dispatch_impl(st_context *ctx, Params &p, int nsrc, int xm) {
     if constexpr (is_i8(FMT)) {
-        if (xm == XM_F32) return launch_gs<FMT, 1, XM_F32, false>(ctx, p);
-        return launch_gs<FMT, 1, XM_F16, false>(ctx, p);
+        if (xm == XM_F32) return launch_fmt<FMT, 1, XM_F32, false>(ctx, p);
+        return launch_fmt<FMT, 1, XM_F16, false>(ctx, p);
     } else {
         if (nsrc == 2) {
-            if (xm == XM_F32) return launch_gs<FMT, 2, XM_F32, PERM>(ctx, p);
-            return launch_gs<FMT, 2, XM_F16, PERM>(ctx, p);
+            if (xm == XM_F32) return launch_fmt<FMT, 2, XM_F32, PERM>(ctx, p);
+            return launch_fmt<FMT, 2, XM_F16, PERM>(ctx, p);
         }
-        if (xm == XM_F32) return launch_gs<FMT, 1, XM_F32, PERM>(ctx, p);
-        if (xm == XM_F16) return launch_gs<FMT, 1, XM_F16, PERM>(ctx, p);
-        return launch_gs<FMT, 1, XM_SILU, PERM>(ctx, p);
+        if (xm == XM_F32) return launch_fmt<FMT, 1, XM_F32, PERM>(ctx, p);
+        if (xm == XM_F16) return launch_fmt<FMT, 1, XM_F16, PERM>(ctx, p);
+        return launch_fmt<FMT, 1, XM_SILU, PERM>(ctx, p);
     }
 }
 

@@ -99,6 +99,20 @@ int st_context_reserve_workspace(st_context *ctx, size_t bytes) {
     return ST_OK;
 }
 
+int st_context_set_tune(st_context *ctx, int knob, int value) {
+    if (!ctx) return st::fail(ST_ERR_INVALID, "st_context_set_tune: ctx is NULL");
+    if (knob < 0 || knob >= ST_TUNE_COUNT) return st::fail(ST_ERR_INVALID, "st_context_set_tune: knob %d", knob);
+    ctx->tune[knob] = value < 0 ? -1 : value;
+    return ST_OK;
+}
+
+int st_context_get_tune(st_context *ctx, int knob, int *value) {
+    if (!ctx || !value) return st::fail(ST_ERR_INVALID, "st_context_get_tune: NULL argument");
+    if (knob < 0 || knob >= ST_TUNE_COUNT) return st::fail(ST_ERR_INVALID, "st_context_get_tune: knob %d", knob);
+    *value = ctx->tune[knob];
+    return ST_OK;
+}
+
 int st_context_destroy(st_context *ctx) {
     if (!ctx) return ST_OK;
     (void)hipSetDevice(ctx->device);

@@ -6,11 +6,12 @@ device, so torch ops and HIP kernels stay ordered without extra syncs.
 """
 from __future__ import annotations
 
+import contextlib
 import ctypes
 
 import numpy as np
 
-from ._lib import call, lib
+from ._lib import TUNE, call, lib
 
 
 def ptr(t) -> int | None:
@@ -46,6 +47,30 @@ class GpuContext:
         if s != self._stream:
             call("st_context_set_stream", self.handle, s)
             self._stream = s
+
+    # -- kernel-path overrides (st_context_set_tune) -------------------------
+    def set_tune(self, knob: str, value: int) -> None:
+        """Force a kernel-path setting of this context (-1 = automatic), e.g.
+        set_tune("DECODE_KERNEL", 1) for the streaming decode kernel."""
+        call("st_context_set_tune", self.handle, TUNE[knob], int(value))
+
+    def get_tune(self, knob: str) -> int:
+        v = ctypes.c_int()
+        call("st_context_get_tune", self.handle, TUNE[knob], ctypes.byref(v))
+        return v.value
+
+    @contextlib.contextmanager
+    def tuning(self, **knobs):
+        """with gpu.tuning(NO_CHUNK=1, ...): the settings hold inside the
+        block and the previous values come back after it."""
+        old = {k: self.get_tune(k) for k in knobs}
+        try:
+            for k, v in knobs.items():
+                self.set_tune(k, v)
+            yield self
+        finally:
+            for k, v in old.items():
+                self.set_tune(k, v)
 
     def reserve_workspace(self, nbytes: int) -> None:
         call("st_context_reserve_workspace", self.handle, nbytes)

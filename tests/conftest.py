@@ -33,3 +33,20 @@ def gpu():
     ctx = GpuContext(0)
     yield ctx
     ctx.close()
+
+
+@pytest.fixture
+def tune(gpu):
+    """tune(KNOB=value, ...): force kernel-path settings of the shared context
+    (st_context_set_tune) for the rest of the test; all restored after it."""
+    from shady_thinker_amd._lib import TUNE_KNOBS
+
+    saved = {k: gpu.get_tune(k) for k in TUNE_KNOBS}
+
+    def set_(**knobs):
+        for k, v in knobs.items():
+            gpu.set_tune(k, int(v))
+
+    yield set_
+    for k, v in saved.items():
+        gpu.set_tune(k, v)

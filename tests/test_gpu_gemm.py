@@ -162,7 +162,7 @@ def test_gemm_graph_replay_matches_eager(gpu, orc):
 
 
 @pytest.mark.parametrize("gs", [64, 128, 256])
-def test_gemm_split_k_matches_unsplit(gpu, orc, gs, monkeypatch):
+def test_gemm_split_k_matches_unsplit(gpu, orc, gs, tune):
     """Small grids split K across workgroups (f32 partials in the context
     workspace, reduced in a fixed order): same result as one workgroup per
     tile up to summation order, and the oracle's."""
@@ -170,7 +170,7 @@ def test_gemm_split_k_matches_unsplit(gpu, orc, gs, monkeypatch):
     c = orc.gptq_case(60 + gs, K, N, gs, zeros=True, act_order=True, M=Mr, x_dtype=np.float16)
     w = up(gpu, c)
     y_split = run_gemm(gpu, w, c["x"])
-    monkeypatch.setenv("ST_GEMM_NO_SPLIT", "1")
+    tune(GEMM_NO_SPLIT=1)
     y_one = run_gemm(gpu, w, c["x"])
     ref = orc.gptq_matvec_f64(c["x"], c["qweight"], c["scales"], K, N, gs, qzeros=c["qzeros"], g_idx=c["g_idx"])
     e_s, e_o, e_so = orc.rel_l2(y_split, ref), orc.rel_l2(y_one, ref), orc.rel_l2(y_split, y_one)
@@ -183,7 +183,7 @@ def test_gemm_split_k_matches_unsplit(gpu, orc, gs, monkeypatch):
     (200, 2048, 776, 64, False, False),
     (129, 1024, 520, 256, True, False),
 ])
-def test_gemm_tile_widths_agree(gpu, orc, Mr, K, N, gs, zeros, act, monkeypatch):
+def test_gemm_tile_widths_agree(gpu, orc, Mr, K, N, gs, zeros, act, tune):
     """128 x 128 workgroup tiles (one 32-column block per wave, chosen for
     small grids) and 128 x 256 tiles give the same C bit for bit (same k
     order per output) and meet the oracle's bar."""
@@ -191,8 +191,8 @@ def test_gemm_tile_widths_agree(gpu, orc, Mr, K, N, gs, zeros, act, monkeypatch)
     w = up(gpu, c)
     ys = {}
     for cb in ("1", "2"):
-        monkeypatch.setenv("ST_GEMM_CB", cb)
-        monkeypatch.setenv("ST_GEMM_NO_SPLIT", "1")
+        tune(GEMM_CB=int(cb))
+        tune(GEMM_NO_SPLIT=1)
         ys[cb] = run_gemm(gpu, w, c["x"])
     ref = orc.gptq_matvec_f64(c["x"], c["qweight"], c["scales"], K, N, gs, qzeros=c["qzeros"], g_idx=c["g_idx"])
     assert np.array_equal(ys["1"], ys["2"])

@@ -1,0 +1,224 @@
+"""GPU parity of the streaming decode kernel (qmv_stream.hpp: weights moved
+HBM -> LDS by per-wave DMA rings, 1-4 tokens, tiled weights), forced through
+the context setting DECODE_KERNEL=1 on every variant it serves, and of the
+decode shapes of configs[4]'s lm_head and o_proj on the entry points' own
+routing. Reference calls: Model::gptq_matvec / fused_silu_gptq_down
+(src/model.rs:357-408) and the int4 lm_head dispatch (src/model.rs:455-468,
+824-834).
+
+Bars: rel-L2 1e-4 against the float64 oracle;
+one-hot inputs return dequantized rows bit for bit. Against the
+register-ring kernel the only difference is the order of the f32 additions
+across groups: rel-L2 below 1e-6.
+"""
+import numpy as np
+import pytest
+import torch
+
+import shady_thinker_amd as sta
+from shady_thinker_amd import model as M
+
+pytestmark = pytest.mark.gpu
+
+TOL = 1e-4  # rel-L2, f32-accumulate matvec (north_star)
+STREAM, RING = 1, 0
+
+
+def up(gpu, case, zeros_plus_one=False):
+    return sta.GptqWeight.upload(gpu, case["qweight"], case["scales"], case["gs"], qzeros=case["qzeros"],
+                                 g_idx=case["g_idx"], zeros_plus_one=zeros_plus_one, tiled=True)
+
+
+def dev(a, dtype=None):
+    t = torch.from_numpy(np.ascontiguousarray(a)).cuda()
+    return t if dtype is None else t.to(dtype)
+
+
+def run(gpu, kind, w, w2, x, b=None):
+    """kind: 'f32' / 'f16' matvec, 'silu' (fused_silu_gptq_down on x, b),
+    'dual' (gate/up)."""
+    K, N = w.K, w.N
+    m = x.size // K
+    y = torch.empty(m, N, device="cuda")
+    if kind == "silu":
+        M.fused_silu_gptq_down(gpu, dev(x), dev(b), w.qweight, w.scales, y, K, N, w.group_size, w.qzeros, w.perm,
+                               w.flags)
+    elif kind == "dual":
+        M.fused_gate_up_silu(gpu, dev(x), w.qweight, w.scales, w2.qweight, w2.scales, y, K, N, w.group_size,
+                             gate_qz=w.qzeros, up_qz=w2.qzeros, perm=w.perm, flags=w.flags)
+    else:
+        xt = dev(x, torch.float16 if kind == "f16" else torch.float32)
+        M.gptq_matvec(gpu, "t", xt, w.qweight, w.scales, y, K, N, w.group_size, w.qzeros, w.perm, w.flags)
+    torch.cuda.synchronize()
+    return y.cpu().numpy()
+
+
+# (K, N, gs, tokens, zeros, zeros+1, act-order, x kind): the layouts of one
+# unit (g64: two 4-byte DMAs, g128: one 16-byte, g256: two 16-byte), tiles
+# split across waves (one tile per workgroup) and many tiles per workgroup,
+# workgroups with fewer units than waves (empty ranges), every x form
+CASES = [
+    (4096, 4096, 128, 1, False, False, False, "f32"),   # q_proj: one tile split over 16 waves
+    (1024, 36880, 64, 3, True, False, True, "f16"),     # 2305 tiles, 9 per workgroup; g64; act-order
+    (4096, 11008, 256, 2, True, True, False, "dual"),   # gate/up, g256, AutoGPTQ-v1 zeros
+    (11008, 4096, 128, 1, False, False, False, "silu"),  # down on silu(a) * b, long K
+    (2048, 2048, 128, 4, True, False, True, "f32"),     # four tokens, act-order
+    (2560, 19456, 128, 1, False, False, False, "dual"),  # configs[4] gate/up
+    (128, 64, 128, 1, False, False, False, "f32"),      # one unit per workgroup: 15 empty waves
+    (256, 48, 64, 2, True, False, False, "f32"),        # 4 groups x 3 tiles < 16 waves
+    (1536, 1024, 256, 3, False, False, True, "silu"),   # silu with act-order, g256
+]
+
+
+@pytest.mark.parametrize("K,N,gs,Mr,zeros,zp1,act,kind", CASES)
+def test_stream_matches_oracle_and_ring(gpu, orc, tune, K, N, gs, Mr, zeros, zp1, act, kind):
+    seed = (K * 7 + N + gs + Mr) % 1000
+    c = orc.gptq_case(seed, K, N, gs, zeros=zeros, act_order=act, M=Mr,
+                      x_dtype=np.float16 if kind == "f16" else np.float32)
+    if zp1 and c["qzeros"] is not None:
+        # stored z - 1 (AutoGPTQ v1): keep every z - 1 in 0..14 so z stays a nibble
+        qz = c["qzeros"].copy()
+        for j in range(8):
+            nib = (qz >> (4 * j)) & 0xF
+            qz = (qz & ~np.uint32(0xF << (4 * j))) | (np.minimum(nib, 14) << (4 * j)).astype(np.uint32)
+        c["qzeros"] = qz
+    w = up(gpu, c, zeros_plus_one=zp1)
+    w2, c2, b = None, None, None
+    if kind == "dual":
+        c2 = orc.gptq_case(seed + 1, K, N, gs, zeros=zeros, act_order=False)
+        c2["g_idx"] = c["g_idx"]  # gate and up share the act-order permutation
+        w2 = up(gpu, c2, zeros_plus_one=zp1)
+    x = c["x"]
+    if kind == "silu":
+        b = orc.normal_f32(seed + 7, Mr * K).reshape(Mr, K)
+    tune(DECODE_KERNEL=STREAM)
+    y = run(gpu, kind, w, w2, x, b)
+    y_again = run(gpu, kind, w, w2, x, b)
+    tune(DECODE_KERNEL=RING)
+    y_ring = run(gpu, kind, w, w2, x, b)
+
+    zo = 1 if zp1 else 0
+    f64 = lambda cc, xx: orc.gptq_matvec_f64(xx, cc["qweight"], cc["scales"], K, N, gs, qzeros=cc["qzeros"],
+                                             g_idx=cc["g_idx"], zero_offset=zo)
+    if kind == "silu":
+        ref = f64(c, orc.silu_mul_f64(x, b))
+    elif kind == "dual":
+        ref = orc.silu_gate_f64(f64(c, x), f64(c2, x))
+    else:
+        ref = f64(c, x)
+    e = orc.rel_l2(y, ref)
+    print(f"stream K={K} N={N} gs={gs} M={Mr} {kind}: rel-L2 {e:.3e} vs ring {orc.rel_l2(y, y_ring):.2e}")
+    assert np.isfinite(y).all() and e < TOL
+    assert np.array_equal(y, y_again)  # deterministic
+    assert orc.rel_l2(y, y_ring) < 1e-6
+
+
+def test_stream_one_hot_returns_dequant_rows(gpu, orc, tune):
+    """x = e_k returns row k of the dequantized matrix bit for bit (every
+    product exact, one rounding of an exact integer sum), for rows in the
+    first, a middle and the last group, through a workgroup whose tile is
+    split across waves."""
+    K, N, gs = 2048, 4096, 128
+    c = orc.gptq_case(301, K, N, gs, zeros=True)
+    w = up(gpu, c)
+    deq = orc.gptq_dequant_f32(c["qweight"], c["scales"], K, N, gs, qzeros=c["qzeros"])
+    ks = [0, 5, 1000, K - 1]
+    x = np.zeros((len(ks), K), np.float32)
+    for i, k in enumerate(ks):
+        x[i, k] = 1.0
+    tune(DECODE_KERNEL=STREAM)
+    y = run(gpu, "f32", w, None, x)
+    for i, k in enumerate(ks):
+        assert np.array_equal(y[i], deq[k]), k
+
+
+@pytest.mark.parametrize("Mr,K,N,f16", [(1, 5120, 13824, True), (3, 1024, 4096, False), (4, 384, 80, True)])
+def test_stream_int8(gpu, orc, tune, Mr, K, N, f16):
+    """INT8 per-channel weights (tiled) on the streaming kernel: f64 oracle
+    and the register-ring kernel."""
+    c = orc.int8_case(310 + Mr, K, N, M=Mr, x_dtype=np.float16 if f16 else np.float32)
+    w = sta.Int8Weight.upload(gpu, c["w"], c["scale"])
+    x = dev(c["x"])
+    y = torch.empty(Mr, N, device="cuda")
+    outs = {}
+    for mode in (STREAM, RING):
+        tune(DECODE_KERNEL=mode, I8MM_MIN_M=99)
+        M.int8_matvec(gpu, x, w.w, w.scale, y, K, N, w.flags)
+        torch.cuda.synchronize()
+        outs[mode] = y.cpu().numpy().copy()
+    ref = orc.int8_matvec_f64(c["x"], c["w"], c["scale"], K, N)
+    assert orc.rel_l2(outs[STREAM], ref) < TOL
+    assert orc.rel_l2(outs[STREAM], outs[RING]) < 1e-6
+
+
+def test_stream_graph_replay(gpu, orc, tune):
+    """The streaming kernel captured in a HIP graph: every replay equals the
+    eager result bit for bit, with eager work on the same weights between
+    replays."""
+    K, N = 2560, 40960
+    c = orc.gptq_case(320, K, N, 128)
+    w = up(gpu, c)
+    tune(DECODE_KERNEL=STREAM)
+    x = dev(c["x"])
+    y = torch.empty(1, N, device="cuda")
+    M.gptq_matvec(gpu, "t", x, w.qweight, w.scales, y, K, N, 128, flags=w.flags)
+    torch.cuda.synchronize()
+    eager = y.clone()
+    s = torch.cuda.Stream()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.stream(s):
+        with torch.cuda.graph(g, stream=s):
+            M.gptq_matvec(gpu, "t", x, w.qweight, w.scales, y, K, N, 128, flags=w.flags)
+    torch.cuda.synchronize()
+    y2 = torch.empty_like(y)
+    for _ in range(3):
+        y.zero_()
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(y, eager)
+        M.gptq_matvec(gpu, "t", x, w.qweight, w.scales, y2, K, N, 128, flags=w.flags)
+        torch.cuda.synchronize()
+
+
+# ---------------------------------------------- configs[4] decode shapes
+H, V, Q = 2560, 151936, 4096
+
+
+@pytest.mark.parametrize("Mr", [1, 16])
+def test_lm_head_int4(gpu, orc, Mr):
+    """configs[4]'s int4 lm_head 2560 -> 151936 (g128) on the entry point's
+    own routing: the streaming kernel at one token, the f16-MFMA kernel at 16
+    (src/model.rs:455-468, 824-834 dispatch the lm_head per token). Batch 1
+    against the f64 oracle over every column; batch 16 over every row and a
+    slice of 8192 columns (the oracle on the same columns of qweight and
+    scales) plus the last 16 columns."""
+    c = orc.gptq_case(330 + Mr, H, V, 128, M=Mr)
+    w = up(gpu, c)
+    y = run(gpu, "f32", w, None, c["x"])
+    if Mr == 1:
+        ref = orc.gptq_matvec_f64(c["x"], c["qweight"], c["scales"], H, V, 128)
+        e = orc.rel_l2(y, ref)
+    else:
+        errs = []
+        for n0, n1 in ((70000, 78192), (V - 16, V)):
+            qw = np.ascontiguousarray(c["qweight"][:, n0:n1])
+            sc = np.ascontiguousarray(c["scales"][:, n0:n1])
+            ref = orc.gptq_matvec_f64(c["x"], qw, sc, H, n1 - n0, 128)
+            errs.append(orc.rel_l2(y[:, n0:n1], ref))
+        e = max(errs)
+    print(f"lm_head int4 M={Mr}: rel-L2 {e:.3e}")
+    assert np.isfinite(y).all() and e < TOL
+
+
+@pytest.mark.parametrize("Mr", [1, 16])
+def test_o_proj_cfg4(gpu, orc, Mr):
+    """configs[4]'s o_proj 4096 -> 2560 (160 tiles, fewer than the CUs) at
+    batch 1 and 16, every row against the f64 oracle."""
+    c = orc.gptq_case(340 + Mr, Q, H, 128, M=Mr)
+    w = up(gpu, c)
+    y = run(gpu, "f32", w, None, c["x"])
+    ref = orc.gptq_matvec_f64(c["x"], c["qweight"], c["scales"], Q, H, 128)
+    e = orc.rel_l2(y, ref)
+    print(f"o_proj M={Mr}: rel-L2 {e:.3e}")
+    assert e < TOL
