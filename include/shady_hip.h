@@ -163,6 +163,23 @@ int st_gptq_i4_matvec(st_context *ctx, const void *x, int x_dtype,
                       const uint32_t *qzeros, const int32_t *perm, float *y,
                       int M, int K, int N, int group_size, uint32_t flags);
 
+/* No counterpart in the reference: for callers that cannot allocate device
+ * memory (code under HIP graph capture, tight serving loops, harnesses that
+ * forbid hipMalloc). st_gptq_i4_matvec with everything its kernels keep
+ * beyond the inputs and outputs (the f16-MFMA kernel's split of f32 x into
+ * f16 rows, split-K partial sums) in a fixed array of
+ * ST_NOALLOC_SCRATCH_BYTES that the library holds on every GPU it runs on,
+ * from the context's creation until the process ends, instead of the
+ * context workspace. Allocates nothing. A call whose scratch would exceed
+ * the array fails with ST_ERR_WORKSPACE and launches nothing. Every call on
+ * one GPU shares that GPU's array (nothing in it needs to start at zero;
+ * each call overwrites what it reads): calls that overlap on one GPU (other
+ * streams or contexts) race. */
+#define ST_NOALLOC_SCRATCH_BYTES (8u << 20)
+int st_gptq_i4_matvec_noalloc(st_context *ctx, const void *x, int x_dtype, const uint32_t *qweight,
+                              const uint16_t *scales, const uint32_t *qzeros, const int32_t *perm, float *y, int M,
+                              int K, int N, int group_size, uint32_t flags);
+
 /* y = (silu(a) * b) . dequant(W), silu(v) = v / (1 + exp(-v)).
  * Replaces Model::fused_silu_gptq_down (src/model.rs:383-408) dispatching
  * fused_silu_gptq(_4t).wgsl (src/shaders/fused_silu_gptq_4t.wgsl:26-81).

@@ -15,6 +15,7 @@ LIB_PATH = os.path.join(HERE, "libshady_hip.so")
 HEADER = os.path.join(ROOT, "include", "shady_hip.h")
 
 ST_OK = 0
+ST_ERR_WORKSPACE = 6
 ST_F32, ST_F16, ST_BF16 = 0, 1, 2
 ST_FLAG_ZEROS_PLUS_ONE = 0x1
 ST_FLAG_TILED = 0x2
@@ -63,6 +64,7 @@ _SIGNATURES = {
     "st_copy": (_I, [_P, _P, _P, _SZ]),
     "st_flush": (_I, [_P]),
     "st_gptq_i4_matvec": (_I, [_P, _P, _I, _P, _P, _P, _P, _P, _I, _I, _I, _I, _U32]),
+    "st_gptq_i4_matvec_noalloc": (_I, [_P, _P, _I, _P, _P, _P, _P, _P, _I, _I, _I, _I, _U32]),
     "st_gptq_i4_silu_matvec": (_I, [_P, _P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _U32]),
     "st_gptq_i4_gate_up_silu": (_I, [_P, _P, _I, _P, _P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _U32]),
     "st_gptq_i4_dequant": (_I, [_P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _U32]),

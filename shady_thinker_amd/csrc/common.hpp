@@ -21,6 +21,9 @@ struct st_context {
     // what it uses; calls on one context are ordered by its stream).
     float *ws = nullptr;
     size_t ws_bytes = 0;
+    // the no-allocation entry point's scratch on this context's GPU (the
+    // device address of runtime.hip's static array)
+    void *scratch = nullptr;
     // kernel-path overrides (st_tune); -1 = automatic
     int tune[ST_TUNE_COUNT];
     st_context() {

@@ -160,6 +160,28 @@ int st_gptq_i4_matvec(st_context *ctx, const void *x, int x_dtype, const uint32_
     return by_token_blocks(ctx, p, xm, [&](QmvParams &q) { return launch_i4(ctx, q, tiled, 1, xm); });
 }
 
+int st_gptq_i4_matvec_noalloc(st_context *ctx, const void *x, int x_dtype, const uint32_t *qweight,
+                              const uint16_t *scales, const uint32_t *qzeros, const int32_t *perm, float *y, int M,
+                              int K, int N, int group_size, uint32_t flags) {
+    if (!ctx) return st::fail(ST_ERR_INVALID, "st_gptq_i4_matvec_noalloc: ctx is NULL");
+    if (!ctx->scratch) return st::fail(ST_ERR_WORKSPACE, "st_gptq_i4_matvec_noalloc: no scratch on this device");
+    // The most any path of the call keeps: the f16-MFMA kernel's split of one
+    // 16-token block of f32 x (2 f16 rows per token and a factor per 128 k);
+    // split-K partials shrink (or go unsplit) to fit what is there.
+    if (M > 0 && K > 0 && x_dtype == ST_F32) {
+        const size_t mb = (size_t)std::min(M, kTokenBlock);
+        const size_t need = 2 * mb * K * 2 + mb * (size_t)(K / 128) * 4;
+        if (need > ST_NOALLOC_SCRATCH_BYTES)
+            return st::fail(ST_ERR_WORKSPACE, "st_gptq_i4_matvec_noalloc: %zu bytes of scratch needed, %u held", need,
+                            (unsigned)ST_NOALLOC_SCRATCH_BYTES);
+    }
+    st_context view = *ctx;  // the same stream and settings, the scratch as workspace
+    view.ws = static_cast<float *>(ctx->scratch);
+    view.ws_bytes = ST_NOALLOC_SCRATCH_BYTES;
+    view.own_stream = false;
+    return st_gptq_i4_matvec(&view, x, x_dtype, qweight, scales, qzeros, perm, y, M, K, N, group_size, flags);
+}
+
 int st_gptq_i4_silu_matvec(st_context *ctx, const float *a, const float *b, const uint32_t *qweight,
                            const uint16_t *scales, const uint32_t *qzeros, const int32_t *perm, float *y, int M, int K,
                            int N, int group_size, uint32_t flags) {

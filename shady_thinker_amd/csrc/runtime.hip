@@ -6,6 +6,7 @@
 
 #include <cstdlib>
 #include <cstring>
+#include <mutex>
 
 namespace st {
 
@@ -26,6 +27,29 @@ void clear_error() { g_last_error.clear(); }
 
 static constexpr size_t kDefaultWorkspace = size_t(64) << 20;
 
+// Scratch of st_gptq_i4_matvec_noalloc: one fixed array per GPU, held from
+// load until the process ends. Host code never passes the array's name (a
+// host-side stand-in, not a device address): each GPU's copy is looked up
+// once, with that device current, and its address kept per device.
+static __device__ __align__(256) unsigned char scratch[ST_NOALLOC_SCRATCH_BYTES];
+static constexpr int kMaxDevices = 64;
+static std::mutex g_scratch_mu;
+static void *g_scratch[kMaxDevices] = {};
+
+// The scratch address on `device` (which must be current).
+static int scratch_for(int device, void **out) {
+    if (device >= kMaxDevices) return st::fail(ST_ERR_UNSUPPORTED, "scratch: device %d >= %d", device, kMaxDevices);
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    if (!g_scratch[device]) {
+        void *ptr = nullptr;
+        hipError_t e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+        if (e != hipSuccess || !ptr) return st::hip_fail(e, "hipGetSymbolAddress(scratch)");
+        g_scratch[device] = ptr;
+    }
+    *out = g_scratch[device];
+    return ST_OK;
+}
+
 extern "C" {
 
 const char *st_last_error(void) { return st::g_last_error.c_str(); }
@@ -45,8 +69,11 @@ int st_context_create(int device, st_context **out) {
     if (std::strncmp(prop.gcnArchName, "gfx950", 6) != 0)
         return st::fail(ST_ERR_UNSUPPORTED, "st_context_create: device is %s, this library is built for gfx950",
                         prop.gcnArchName);
+    void *scr = nullptr;
+    if (int rc = scratch_for(device, &scr)) return rc;
     st_context *ctx = new st_context();
     ctx->device = device;
+    ctx->scratch = scr;
     ctx->num_cus = prop.multiProcessorCount;
     hipError_t e = hipStreamCreateWithFlags(&ctx->stream, hipStreamNonBlocking);
     if (e != hipSuccess) {
