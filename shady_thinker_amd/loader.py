@@ -26,7 +26,7 @@ from dataclasses import dataclass, field
 
 import numpy as np
 
-from .weights import GptqWeight, QuantConfig
+from .weights import GptqWeight, QuantConfig, check_gptq_tensors
 
 _GPTQ_PARTS = ("qweight", "scales", "qzeros", "g_idx")
 
@@ -74,7 +74,9 @@ def read_gptq_checkpoint(model_dir: str) -> GptqCheckpoint:
                 stem, _, part = name.rpartition(".")
                 if part in _GPTQ_PARTS:
                     t = f.get_tensor(name)
-                    ck.linears.setdefault(stem, {})[part] = t.numpy() if t.dtype != _bf16() else None
+                    if t.dtype == _bf16():
+                        raise ValueError(f"{name}: bfloat16; GPTQ {part} must be float16 (scales) or integer")
+                    ck.linears.setdefault(stem, {})[part] = t.numpy()
                 elif part == "weight" and ("lm_head" in stem or "embed_tokens" in stem):
                     t = f.get_tensor(name)
                     if t.dtype == _bf16() and t.dim() == 2:
@@ -90,6 +92,10 @@ def read_gptq_checkpoint(model_dir: str) -> GptqCheckpoint:
         K = qw.shape[0] * 8
         if K % sc.shape[0] or K // sc.shape[0] != qc.group_size:
             raise ValueError(f"{stem}: K={K} with {sc.shape[0]} groups, quantize_config group_size={qc.group_size}")
+        try:
+            check_gptq_tensors(qw, sc, qc.group_size, parts.get("qzeros"), parts.get("g_idx"))
+        except ValueError as e:
+            raise ValueError(f"{stem}: {e}") from None
     return ck
 
 

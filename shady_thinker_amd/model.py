@@ -14,7 +14,7 @@ qweight int32 [K/8, N], scales f16 [K/gs, N], optional qzeros int32
 """
 from __future__ import annotations
 
-from ._lib import ST_F16, ST_F32, call
+from ._lib import ST_F16, ST_F32, ST_FLAG_TILED, call, lib
 from .gpu import ptr
 from .weights import GptqWeight, Int8Weight
 
@@ -35,10 +35,52 @@ def _rows(t, k: int) -> int:
     return t.numel() // k
 
 
+# Argument checks the C ABI cannot make: it receives bare pointers, so a
+# wrong dtype or a short buffer would be read or written past its end on the
+# device. Every helper checks its tensors here before the call.
+def _need(t, name: str, dtypes, numel: int) -> None:
+    if t is None:
+        raise ValueError(f"{name} is required")
+    if t.dtype not in dtypes:
+        raise TypeError(f"{name}: dtype {t.dtype} (need {' or '.join(str(d) for d in dtypes)})")
+    if not t.is_contiguous():
+        raise ValueError(f"{name}: not contiguous")
+    if t.numel() < numel:
+        raise ValueError(f"{name}: {t.numel()} elements, need at least {numel}")
+
+
+def _torch():
+    import torch
+
+    return torch
+
+
+def _check_gptq(qweight, scales, qzeros, perm, k: int, n: int, group_size: int, flags: int) -> None:
+    torch = _torch()
+    if group_size <= 0 or k <= 0 or n <= 0 or k % group_size or k % 8 or n % 8:
+        raise ValueError(f"GPTQ weight {k} x {n}, group size {group_size}: K and N multiples of 8, K of the group")
+    words = lib().st_gptq_i4_tiled_words(k, n, group_size) if flags & ST_FLAG_TILED else k // 8 * n
+    _need(qweight, "qweight", (torch.int32,), words)
+    _need(scales, "scales", (torch.float16,), k // group_size * n)
+    if qzeros is not None:
+        _need(qzeros, "qzeros", (torch.int32,), k // group_size * (n // 8))
+    if perm is not None:
+        _need(perm, "perm", (torch.int32,), k)
+
+
+def _check_io(x, k: int, out, n: int, x_dtypes=None, out_dtypes=None, name: str = "input") -> int:
+    torch = _torch()
+    _need(x, name, x_dtypes or (torch.float32, torch.float16), 0)
+    m = _rows(x, k)
+    _need(out, "output", out_dtypes or (torch.float32,), m * n)
+    return m
+
+
 def gptq_matvec(gpu, name: str, input, qweight, scales, output, k: int, n: int, group_size: int = 128,
                 qzeros=None, perm=None, flags: int = 0) -> None:
     """output[M, n] = input[M, k] . dequant(W)  (src/model.rs:357-381)."""
-    m = _rows(input, k)
+    _check_gptq(qweight, scales, qzeros, perm, k, n, group_size, flags)
+    m = _check_io(input, k, output, n)
     gpu.sync_stream()
     call("st_gptq_i4_matvec", gpu.handle, ptr(input), _xdtype(input), ptr(qweight), ptr(scales), ptr(qzeros),
          ptr(perm), ptr(output), m, k, n, group_size, flags)
@@ -47,7 +89,10 @@ def gptq_matvec(gpu, name: str, input, qweight, scales, output, k: int, n: int, 
 def fused_silu_gptq_down(gpu, gate_out, up_out, down_qw, down_sc, output, k: int, n: int, group_size: int = 128,
                          qzeros=None, perm=None, flags: int = 0) -> None:
     """output = (silu(gate_out) * up_out) . dequant(W_down)  (src/model.rs:383-408)."""
-    m = _rows(gate_out, k)
+    torch = _torch()
+    _check_gptq(down_qw, down_sc, qzeros, perm, k, n, group_size, flags)
+    m = _check_io(gate_out, k, output, n, x_dtypes=(torch.float32,), name="gate_out")
+    _need(up_out, "up_out", (torch.float32,), m * k)
     gpu.sync_stream()
     call("st_gptq_i4_silu_matvec", gpu.handle, ptr(gate_out), ptr(up_out), ptr(down_qw), ptr(down_sc),
          ptr(qzeros), ptr(perm), ptr(output), m, k, n, group_size, flags)
@@ -56,7 +101,9 @@ def fused_silu_gptq_down(gpu, gate_out, up_out, down_qw, down_sc, output, k: int
 def fused_gate_up_silu(gpu, input, gate_qw, gate_sc, up_qw, up_sc, output, k: int, n: int, group_size: int = 128,
                        gate_qz=None, up_qz=None, perm=None, flags: int = 0) -> None:
     """output = silu(input . Wg) * (input . Wu)  (fused_gate_up_silu_4t.wgsl)."""
-    m = _rows(input, k)
+    _check_gptq(gate_qw, gate_sc, gate_qz, perm, k, n, group_size, flags)
+    _check_gptq(up_qw, up_sc, up_qz, perm, k, n, group_size, flags)
+    m = _check_io(input, k, output, n)
     gpu.sync_stream()
     call("st_gptq_i4_gate_up_silu", gpu.handle, ptr(input), _xdtype(input), ptr(gate_qw), ptr(gate_sc),
          ptr(gate_qz), ptr(up_qw), ptr(up_sc), ptr(up_qz), ptr(perm), ptr(output), m, k, n, group_size, flags)
@@ -71,6 +118,10 @@ def gptq_dequant(gpu, qweight, scales, out, k: int, n: int, group_size: int = 12
     od = {torch.float32: 0, torch.bfloat16: 2}.get(out.dtype)
     if od is None:
         raise TypeError(f"dequant output dtype {out.dtype}")
+    if g_idx is not None:
+        _need(g_idx, "g_idx", (torch.int32,), k)
+    _check_gptq(qweight, scales, qzeros, None, k, n, group_size, flags)
+    _need(out, "out", (out.dtype,), k * n)
     gpu.sync_stream()
     call("st_gptq_i4_dequant", gpu.handle, ptr(qweight), ptr(scales), ptr(qzeros), ptr(g_idx), ptr(out), od, k, n,
          group_size, flags)
@@ -79,7 +130,11 @@ def gptq_dequant(gpu, qweight, scales, out, k: int, n: int, group_size: int = 12
 def int8_matvec(gpu, x, w, scale, y, k: int, n: int, flags: int = 0) -> None:
     """y[M, n] = x[M, k] . (w[n, k]^T * scale[n]) (INT8 per-channel); flags
     ST_FLAG_TILED when w is in the layout of st_int8_repack."""
-    m = _rows(x, k)
+    torch = _torch()
+    m = _check_io(x, k, y, n)
+    nbytes = lib().st_int8_tiled_bytes(k, n) if flags & ST_FLAG_TILED else k * n
+    _need(w, "w", (torch.int8,), nbytes)
+    _need(scale, "scale", (torch.float32,), n)
     gpu.sync_stream()
     call("st_int8_matvec", gpu.handle, ptr(x), _xdtype(x), ptr(w), ptr(scale), ptr(y), m, k, n, flags)
 
@@ -89,10 +144,9 @@ def gptq_gemm(gpu, a, qweight, scales, c, k: int, n: int, group_size: int = 128,
     """c[M, n] = a[M, k] (f16) . dequant(W), c float32 or float16."""
     import torch
 
-    m = _rows(a, k)
-    cd = {torch.float32: ST_F32, torch.float16: ST_F16}.get(c.dtype)
-    if cd is None:
-        raise TypeError(f"gemm output dtype {c.dtype}")
+    _check_gptq(qweight, scales, qzeros, perm, k, n, group_size, flags)
+    m = _check_io(a, k, c, n, x_dtypes=(torch.float16,), out_dtypes=(torch.float32, torch.float16), name="a")
+    cd = ST_F32 if c.dtype == torch.float32 else ST_F16
     gpu.sync_stream()
     call("st_gptq_i4_gemm", gpu.handle, ptr(a), ptr(qweight), ptr(scales), ptr(qzeros), ptr(perm), ptr(c), cd, m,
          k, n, group_size, flags)
@@ -105,12 +159,13 @@ def fused_silu_gptq_gemm(gpu, gate_out, up_out, down_qw, down_sc, output, k: int
     prefill GEMM; gate_out and up_out f16, output float32 or float16."""
     import torch
 
-    m = _rows(gate_out, k)
-    if up_out.shape != gate_out.shape or gate_out.dtype != torch.float16 or up_out.dtype != torch.float16:
-        raise TypeError("gate_out and up_out: float16 tensors of one shape")
-    cd = {torch.float32: ST_F32, torch.float16: ST_F16}.get(output.dtype)
-    if cd is None:
-        raise TypeError(f"gemm output dtype {output.dtype}")
+    _check_gptq(down_qw, down_sc, qzeros, perm, k, n, group_size, flags)
+    m = _check_io(gate_out, k, output, n, x_dtypes=(torch.float16,), out_dtypes=(torch.float32, torch.float16),
+                  name="gate_out")
+    if up_out.shape != gate_out.shape:
+        raise ValueError("gate_out and up_out: float16 tensors of one shape")
+    _need(up_out, "up_out", (torch.float16,), m * k)
+    cd = ST_F32 if output.dtype == torch.float32 else ST_F16
     gpu.sync_stream()
     call("st_gptq_i4_silu_gemm", gpu.handle, ptr(gate_out), ptr(up_out), ptr(down_qw), ptr(down_sc), ptr(qzeros),
          ptr(perm), ptr(output), cd, m, k, n, group_size, flags)
@@ -121,9 +176,8 @@ def bf16_matvec(gpu, x, w, y, k: int, n: int) -> None:
     src/model.rs:455-468 / bf16_matvec.wgsl). x f32 or f16, y f32, M <= 8."""
     import torch
 
-    m = _rows(x, k)
-    if w.dtype not in (torch.bfloat16, torch.int16, torch.uint16):
-        raise TypeError(f"bf16 weight dtype {w.dtype}")
+    m = _check_io(x, k, y, n)
+    _need(w, "w", (torch.bfloat16, torch.int16, torch.uint16), n * k)
     gpu.sync_stream()
     call("st_bf16_matvec", gpu.handle, ptr(x), _xdtype(x), ptr(w), ptr(y), m, k, n)
 
@@ -131,11 +185,13 @@ def bf16_matvec(gpu, x, w, y, k: int, n: int) -> None:
 # ---------------------------------------------------------- weight objects
 def linear(gpu, x, w, y) -> None:
     """Dispatch on the weight type: GptqWeight -> st_gptq_i4_matvec (M <= 32)
-    or the prefill GEMM (M > 32, f16 x); Int8Weight -> st_int8_matvec."""
+    or the prefill GEMM (M > 32: it computes on f16 activations, so f32 x is
+    rounded to f16 first); Int8Weight -> st_int8_matvec."""
     if isinstance(w, GptqWeight):
         m = _rows(x, w.K)
         if m > 32:
-            gptq_gemm(gpu, x, w.qweight, w.scales, y, w.K, w.N, w.group_size, w.qzeros, w.perm, w.flags)
+            xa = x if x.dtype == _torch().float16 else x.to(_torch().float16)
+            gptq_gemm(gpu, xa, w.qweight, w.scales, y, w.K, w.N, w.group_size, w.qzeros, w.perm, w.flags)
         else:
             gptq_matvec(gpu, "linear", x, w.qweight, w.scales, y, w.K, w.N, w.group_size, w.qzeros, w.perm, w.flags)
     elif isinstance(w, Int8Weight):

@@ -52,6 +52,40 @@ def _identity_groups(g_idx: np.ndarray, gs: int) -> bool:
     return bool(np.array_equal(g_idx, np.arange(g_idx.size, dtype=np.int64) // gs))
 
 
+def check_gptq_tensors(qweight, scales, group_size: int, qzeros=None, g_idx=None):
+    """Validate a GPTQ linear's checkpoint tensors before they reach the
+    kernels (which take bare pointers): qweight 32-bit [K/8, N], scales f16
+    [K/group_size, N] (the reference reads them as f16 pairs,
+    src/shaders/gptq_matvec.wgsl:5-9; other dtypes are refused, not
+    converted), qzeros 32-bit [K/group_size, N/8], g_idx [K]. Returns
+    (qweight u32, scales u16 bits, qzeros u32 or None, g_idx or None) as
+    contiguous arrays."""
+    qw = np.ascontiguousarray(qweight)
+    if qw.ndim != 2 or qw.dtype.itemsize != 4 or qw.dtype.kind not in "iu":
+        raise ValueError(f"qweight: {qw.dtype} {qw.shape}, need a 2-D int32/uint32 [K/8, N]")
+    K, N = qw.shape[0] * 8, qw.shape[1]
+    if group_size not in (64, 128, 256) or K % group_size:
+        raise ValueError(f"group_size {group_size} with K={K} (group sizes 64, 128, 256 dividing K)")
+    G = K // group_size
+    sc = np.ascontiguousarray(scales)
+    if sc.dtype not in (np.float16, np.uint16):
+        raise ValueError(f"scales: dtype {sc.dtype}, need float16 (convert the checkpoint's scales explicitly)")
+    if sc.shape != (G, N):
+        raise ValueError(f"scales: shape {sc.shape}, need {(G, N)}")
+    qz = None
+    if qzeros is not None:
+        qz = np.ascontiguousarray(qzeros)
+        if qz.dtype.itemsize != 4 or qz.dtype.kind not in "iu" or qz.shape != (G, N // 8) or N % 8:
+            raise ValueError(f"qzeros: {qz.dtype} {qz.shape}, need int32/uint32 {(G, N // 8)}")
+        qz = qz.view(np.uint32)
+    gi = None
+    if g_idx is not None:
+        gi = np.ascontiguousarray(g_idx)
+        if gi.ndim != 1 or gi.size != K or gi.dtype.kind not in "iu":
+            raise ValueError(f"g_idx: {gi.dtype} {gi.shape}, need an integer vector of length K={K}")
+    return qw.view(np.uint32), sc.view(np.uint16), qz, gi
+
+
 @dataclass
 class GptqWeight:
     """One GPTQ int4 linear resident in HBM.
@@ -81,12 +115,11 @@ class GptqWeight:
         repack qweight into the decode kernels' tiled layout (values
         unchanged); otherwise keep the [K/8, N] reference layout."""
         torch = gpu.torch
-        qw = np.ascontiguousarray(qweight).view(np.uint32)
+        qw, sc, qzeros, g_idx = check_gptq_tensors(qweight, scales, group_size, qzeros, g_idx)
         K, N = qw.shape[0] * 8, qw.shape[1]
-        sc = np.ascontiguousarray(scales).view(np.uint16)
         d_qw = gpu.upload_array(qw.view(np.int32), torch.int32)
         d_sc = gpu.upload_array(sc.view(np.float16), torch.float16)
-        d_qz = None if qzeros is None else gpu.upload_array(np.ascontiguousarray(qzeros).view(np.int32), torch.int32)
+        d_qz = None if qzeros is None else gpu.upload_array(qzeros.view(np.int32), torch.int32)
         d_perm = None
         if g_idx is not None and not _identity_groups(np.asarray(g_idx), group_size):
             d_gi = gpu.upload_array(np.ascontiguousarray(g_idx, dtype=np.int32), torch.int32)

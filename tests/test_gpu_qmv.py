@@ -269,12 +269,18 @@ def test_bad_shapes_raise(gpu, orc):
     w = up(gpu, c)
     x = torch.zeros(256, device="cuda")
     y = torch.empty(64, device="cuda")
+    gpu.sync_stream()
+    # an unsupported group size, at the C ABI (the Python helper refuses it
+    # earlier: its scales would be too short)
+    rc = sta._lib.lib().st_gptq_i4_matvec(gpu.handle, x.data_ptr(), 0, w.qweight.data_ptr(), w.scales.data_ptr(),
+                                          None, None, y.data_ptr(), 1, 256, 64, 32, w.flags)
+    assert rc == 2  # ST_ERR_SHAPE
+    with pytest.raises(ValueError):
+        M.gptq_matvec(gpu, "t", x, w.qweight, w.scales, y, 256, 64, 32, flags=w.flags)
     with pytest.raises(sta.ShadyHipError) as ei:
-        M.gptq_matvec(gpu, "t", x, w.qweight, w.scales, y, 256, 64, 32, flags=w.flags)  # unsupported group size
+        M.gptq_matvec(gpu, "t", torch.zeros(40 * 256, device="cuda"), w.qweight, w.scales,
+                      torch.empty(40 * 64, device="cuda"), 256, 64, 128, flags=w.flags)  # M=40
     assert ei.value.code == 2
-    with pytest.raises(sta.ShadyHipError):
-        M.gptq_matvec(gpu, "t", torch.zeros(40 * 256, device="cuda"), w.qweight, w.scales, y, 256, 64, 128,
-                      flags=w.flags)  # M=40
 
 
 def test_dequant_kernel_bit_exact(gpu, orc):
