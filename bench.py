@@ -127,6 +127,22 @@ class Replayer:
         return e0.elapsed_time(e1) / iters
 
 
+def time_replays(torch, g, iters, warmup):
+    """ms per replay of a captured graph (a StackGraph), events on the
+    current stream around exactly `iters` replays."""
+    for _ in range(warmup):
+        g.replay()
+    s = torch.cuda.current_stream()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    e0.record(s)
+    for _ in range(iters):
+        g.replay()
+    e1.record(s)
+    torch.cuda.synchronize()
+    return e0.elapsed_time(e1) / iters
+
+
 def cpu_baseline(seconds=10.0):
     """Oracle restatement of gptq_matvec_4t (src/shaders/gptq_matvec_4t.wgsl)
     on the host cores, q_proj shape (4096 x 4096, f32 x), repeated for about
@@ -316,6 +332,7 @@ def main():
     if not args.no_gemm:
         out["gemm"] = bench_gemm(torch, dev, gpu, Mdl, gen, args)
     out["lm_head_bf16"] = bench_lm_head(torch, dev, gpu, Mdl, gen, args)
+    out["lm_head_int4"] = bench_lm_head_int4(torch, dev, gpu, Mdl, gen, args)
     out["int8_cfg2"] = bench_int8(torch, dev, gpu, Mdl, gen, args)
     if not args.no_stack:
         out["stack_cfg4"] = bench_stack(torch, dev, gpu, Mdl, gen, args)
@@ -360,11 +377,11 @@ def bench_stack(torch, dev, gpu, Mdl, gen, args):
     """the quantized linear stack of a 36-layer decoder
     (hidden 2560, 32 q / 8 kv heads of 128, intermediate 9728, vocab 151936),
     every linear GPTQ int4 g128 (lm_head included), random-init packed
-    weights (2.07 GB: each token streams them from HBM). A token = per layer
-    DecoderLinears.decode (q|k|v, o, fused gate/up emitting silu(g)*u, down
-    on it), then the lm_head; captured as one HIP graph and replayed; batch
-    1 and 16. Attention and norms are outside the path, so activations are
-    synthetic and fixed."""
+    weights (2.07 GB: each token streams them from HBM). A token = one
+    DecoderStack step (per layer q|k|v as one concatenated linear, o, fused
+    gate/up emitting silu(g)*u, down on it; then the lm_head), captured once
+    with DecoderStack.capture and replayed; batch 1 and 16. Attention and
+    norms are outside the path (no hooks), so activations are synthetic."""
     H, Q, KV, I, V, L = 2560, 4096, 1024, 9728, 151936, 36
     TF = sta_flags_tiled()
     import shady_thinker_amd as sta
@@ -380,24 +397,15 @@ def bench_stack(torch, dev, gpu, Mdl, gen, args):
     lm = make_gptq(torch, dev, H, V, gen, gpu)
     per_layer = (decode_bytes(H, Q, 4, Q) + 2 * decode_bytes(H, KV, 4, KV) + decode_bytes(Q, H, 4, H) +
                  decode_bytes(H, 2 * I, 4, I) + decode_bytes(I, H, 4, H))
-    out = {"layers": L, "weights_GB": None}
+    out = {"layers": L, "weights_GB": None, "api": "DecoderStack.capture (one HIP graph per token step)"}
+    stack = sta.DecoderStack(layers, sta.GptqWeight(lm[0], lm[1], None, None, H, V, GS, TF))
     wbytes = 0
     for Mb in (1, 16):
-        x = torch.randn(Mb, H, device=dev, generator=gen)
-        attn = torch.randn(Mb, Q, device=dev, generator=gen)
-        yqkv = torch.empty(Mb, Q + 2 * KV, device=dev)
-        yo = torch.empty(Mb, H, device=dev)
-        h = torch.empty(Mb, I, device=dev)
-        yd = torch.empty(Mb, H, device=dev)
-        logits = torch.empty(Mb, V, device=dev)
-
-        def token(i):
-            for layer in layers:
-                layer.decode(gpu, x, attn, yqkv, yo, h, yd)
-            Mdl.gptq_matvec(gpu, "lm_head", x, lm[0], lm[1], logits, H, V, GS, flags=TF)
-
-        iters = max(10, min(50, args.steps // 4))
-        ms = Replayer(torch, token, 1).run(iters, 3)
+        b = stack.buffers(gpu, Mb)
+        for t in (b.x, b.attn, b.xm):
+            t.normal_(generator=gen)
+        g = stack.capture(gpu, b)
+        ms = time_replays(torch, g, max(10, min(50, args.steps // 4)), 3)
         # algorithmic bytes of one step: the weights (read once for all Mb
         # tokens) plus batch-1 activation terms (Mb - 1 more rows are < 0.1%)
         tok_bytes = L * per_layer + decode_bytes(H, V, 4, V)
@@ -406,6 +414,7 @@ def bench_stack(torch, dev, gpu, Mdl, gen, args):
                              "GB/s": round(tok_bytes / (ms * 1e-3) / 1e9, 1),
                              "hbm_frac": round(tok_bytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
                              "linear_calls_per_step": 4 * L + 1, "qkv": "one concatenated linear"}
+        del g, b
     # Prefill of a 512-token prompt through the same weights with the GEMM
     # (DecoderLinears.prefill: f16 activations and outputs; q|k|v, o, gate,
     # up, and down on silu(gate) * up fused into the GEMM's A pass), then the
@@ -484,6 +493,28 @@ def bench_lm_head(torch, dev, gpu, Mdl, gen, args):
     del w
     return {"N": N, "K": K, "ms": round(ms, 4), "bytes": b, "GB/s": round(b / (ms * 1e-3) / 1e9, 1),
             "hbm_frac": round(b / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)}
+
+
+def bench_lm_head_int4(torch, dev, gpu, Mdl, gen, args):
+    """configs[4]'s lm_head as GPTQ int4 g128 (2560 -> 151936, 200 MB;
+    st_gptq_i4_matvec, the streaming kernel at 1-4 tokens), 4 cold copies
+    (800 MB, three times the MALL), batch 1 and 4."""
+    K, N = 2560, 151936
+    TF = sta_flags_tiled()
+    copies = 4
+    W = [make_gptq(torch, dev, K, N, gen, gpu) for _ in range(copies)]
+    out = {"N": N, "K": K}
+    for Mr in (1, 4):
+        x = torch.randn(Mr, K, device=dev, generator=gen)
+        y = torch.empty(Mr, N, device=dev)
+        iters = max(8, min(48, args.steps // 4))
+        ms = Replayer(torch, lambda i: Mdl.gptq_matvec(gpu, "lm_head", x, W[i % copies][0], W[i % copies][1], y, K,
+                                                       N, GS, flags=TF), copies).run(iters, 4)
+        b = decode_bytes(K, N, 4, N) + (Mr - 1) * (K * 4 + N * 4)
+        out[f"M{Mr}"] = {"ms": round(ms, 5), "bytes": b, "GB/s": round(b / (ms * 1e-3) / 1e9, 1),
+                         "hbm_frac": round(b / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)}
+    del W
+    return out
 
 
 if __name__ == "__main__":

@@ -17,6 +17,10 @@ the same calls for a block of tokens:
 
 Attention, norms and residuals sit between these calls in a model and are
 not part of this path; the caller passes their outputs in.
+
+`DecoderStack` runs the projections of all layers and the lm_head as one
+token step, eagerly or as one captured HIP graph, with the caller's ops
+(norms, attention, residual adds) as capturable hooks between them.
 """
 from __future__ import annotations
 
@@ -25,6 +29,7 @@ from .weights import GptqWeight
 
 _DECODE_MAX = 32     # tokens per decode call (st_gptq_i4_matvec)
 _GATE_UP_BLOCK = 16  # tokens per st_gptq_i4_gate_up_silu call
+_BF16_BLOCK = 8      # tokens per st_bf16_matvec call
 
 
 class DecoderLinears:
@@ -92,3 +97,138 @@ class DecoderLinears:
         d = self.down
         M.fused_silu_gptq_gemm(gpu, gate_out, up_out, d.qweight, d.scales, down_out, d.K, d.N, d.group_size,
                                d.qzeros, d.perm, d.flags)
+
+
+class StackBuffers:
+    """Activation buffers of one decode step of a DecoderStack (device
+    tensors, f32, `batch` rows): x (normed hidden, input of q|k|v), qkv
+    (q, k, v side by side), attn (attention output, input of o), o, xm
+    (normed hidden of the MLP, input of gate/up), h = silu(gate) * up,
+    down, logits."""
+
+    def __init__(self, gpu, stack: "DecoderStack", batch: int):
+        torch = gpu.torch
+        L0 = stack.layers[0]
+        mk = lambda n: torch.zeros(batch, n, device=gpu.device)
+        self.batch = batch
+        self.x, self.qkv, self.attn = mk(L0.hidden), mk(L0.qkv.N), mk(L0.attn_dim)
+        self.o, self.xm, self.h, self.down = mk(L0.hidden), mk(L0.hidden), mk(L0.inter), mk(L0.hidden)
+        self.logits = mk(stack.vocab)
+
+
+class DecoderStack:
+    """The quantized linears of a whole decoder, layer after layer, then the
+    lm_head: one token step, run eagerly (`step`) or captured once as a HIP
+    graph and replayed per token (`capture`). The reference walks this loop
+    on the host and submits once per linear (src/model.rs:348-353, 682-817:
+    q/k/v :698-714, o :727-729, gate/up/down :803-812, lm_head :824-834).
+
+    Between the projections a model runs its own ops (norms, attention,
+    residual adds: src/model.rs:685-690, 724, 799-802, 820-823). They are
+    outside this path and come in as `hooks`, an object with any of these
+    methods, each called with (layer index, StackBuffers) and captured into
+    the same graph (so they must be capturable stream work, e.g. torch ops
+    on the buffers):
+      pre_attention(i, b)   fill b.x (layer 0: from the embedding; later:
+                            add_rmsnorm of the residual and b.down)
+      attention(i, b)       b.qkv -> b.attn
+      post_attention(i, b)  b.o (+ residual) -> b.xm
+      final(b)              b.down (+ residual) -> b.x, the lm_head's input
+    Without hooks the projections run on the buffers as they are (the
+    benchmark's synthetic activations); gate/up then reads b.xm and the
+    lm_head b.x."""
+
+    def __init__(self, layers: list, lm_head):
+        if not layers:
+            raise ValueError("DecoderStack: no layers")
+        L0 = layers[0]
+        for L in layers:
+            if (L.hidden, L.attn_dim, L.inter, L.qkv.N) != (L0.hidden, L0.attn_dim, L0.inter, L0.qkv.N):
+                raise ValueError("DecoderStack: layers of different shapes")
+        self.layers = layers
+        self.lm_head = lm_head
+        if isinstance(lm_head, GptqWeight):
+            if lm_head.K != L0.hidden:
+                raise ValueError("DecoderStack: lm_head K differs from the hidden size")
+            self.vocab = lm_head.N
+        else:  # bf16 [vocab, hidden] (int16 / bfloat16 tensor)
+            if lm_head.dim() != 2 or lm_head.shape[1] != L0.hidden:
+                raise ValueError("DecoderStack: bf16 lm_head must be [vocab, hidden]")
+            self.vocab = lm_head.shape[0]
+
+    def buffers(self, gpu, batch: int) -> StackBuffers:
+        if not 1 <= batch <= _DECODE_MAX:
+            raise ValueError(f"DecoderStack: batch {batch} (1..{_DECODE_MAX})")
+        return StackBuffers(gpu, self, batch)
+
+    def nbytes(self) -> int:
+        lm = self.lm_head.nbytes if isinstance(self.lm_head, GptqWeight) else self.lm_head.numel() * 2
+        return sum(L.nbytes() for L in self.layers) + lm
+
+    def step(self, gpu, b: StackBuffers, hooks=None) -> None:
+        """One token step (all layers, then the lm_head) on b, eagerly."""
+        hk = lambda name: getattr(hooks, name, None) if hooks is not None else None
+        pre, att, post, fin = hk("pre_attention"), hk("attention"), hk("post_attention"), hk("final")
+        m = b.batch
+        for i, L in enumerate(self.layers):
+            if pre:
+                pre(i, b)
+            w = L.qkv
+            M.gptq_matvec(gpu, "qkv_proj", b.x, w.qweight, w.scales, b.qkv, w.K, w.N, w.group_size, w.qzeros, w.perm,
+                          w.flags)
+            if att:
+                att(i, b)
+            w = L.o
+            M.gptq_matvec(gpu, "o_proj", b.attn, w.qweight, w.scales, b.o, w.K, w.N, w.group_size, w.qzeros, w.perm,
+                          w.flags)
+            if post:
+                post(i, b)
+            g, u = L.gate, L.up
+            for r0 in range(0, m, _GATE_UP_BLOCK):
+                r1 = min(m, r0 + _GATE_UP_BLOCK)
+                M.fused_gate_up_silu(gpu, b.xm[r0:r1], g.qweight, g.scales, u.qweight, u.scales, b.h[r0:r1], g.K, g.N,
+                                     g.group_size, gate_qz=g.qzeros, up_qz=u.qzeros, perm=g.perm, flags=g.flags)
+            w = L.down
+            M.gptq_matvec(gpu, "down_proj", b.h, w.qweight, w.scales, b.down, w.K, w.N, w.group_size, w.qzeros,
+                          w.perm, w.flags)
+        if fin:
+            fin(b)
+        lm = self.lm_head
+        if isinstance(lm, GptqWeight):
+            M.gptq_matvec(gpu, "lm_head", b.x, lm.qweight, lm.scales, b.logits, lm.K, lm.N, lm.group_size, lm.qzeros,
+                          lm.perm, lm.flags)
+        else:
+            for r0 in range(0, m, _BF16_BLOCK):
+                r1 = min(m, r0 + _BF16_BLOCK)
+                M.bf16_matvec(gpu, b.x[r0:r1], lm, b.logits[r0:r1], lm.shape[1], lm.shape[0])
+
+    def capture(self, gpu, b: StackBuffers, hooks=None) -> "StackGraph":
+        """Record one token step as a HIP graph on a side stream (the calls
+        are warmed up eagerly first, outside the capture). Replaying it runs
+        the whole step on the buffers in b with one launch from the host."""
+        torch = gpu.torch
+        stream = torch.cuda.Stream(device=gpu.device)
+        stream.wait_stream(torch.cuda.current_stream(gpu.device))
+        with torch.cuda.stream(stream):
+            self.step(gpu, b, hooks)  # warm-up: first-call set-up happens outside the capture
+        torch.cuda.current_stream(gpu.device).wait_stream(stream)
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.stream(stream):
+            with torch.cuda.graph(graph, stream=stream):
+                self.step(gpu, b, hooks)
+        torch.cuda.current_stream(gpu.device).wait_stream(stream)
+        gpu.sync_stream()
+        return StackGraph(graph, b)
+
+
+class StackGraph:
+    """A captured DecoderStack step; replay() runs it on torch's current
+    stream order (the graph's buffers are the StackBuffers it was captured
+    with)."""
+
+    def __init__(self, graph, buffers: StackBuffers):
+        self.graph = graph
+        self.buffers = buffers
+
+    def replay(self) -> None:
+        self.graph.replay()
