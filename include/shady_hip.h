@@ -110,6 +110,8 @@ typedef enum {
     ST_TUNE_I8MM_MIN_M,        /* INT8 decode: fewest tokens for the f16-MFMA kernel */
     ST_TUNE_GEMM_CB,           /* prefill GEMM: 32-column blocks per wave (1 or 2) */
     ST_TUNE_GEMM_NO_SPLIT,     /* 1: prefill GEMM without split-K */
+    ST_TUNE_STREAM_WAVES,      /* streaming decode kernel: waves per workgroup (8 or 16) */
+    ST_TUNE_STREAM_TILES_WG,   /* streaming decode kernel: 16-column tiles per workgroup (0: a workgroup per CU) */
     ST_TUNE_COUNT
 } st_tune;
 int st_context_set_tune(st_context *ctx, int knob, int value);

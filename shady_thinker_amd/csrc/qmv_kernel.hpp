@@ -1099,10 +1099,10 @@ namespace qmv {
 
 // 1-4 tokens on tiled weights: the streaming kernel (qmv_stream.hpp) from
 // this many 16-column tiles per CU on (graph replay, one token: the int4
-// lm_head 2560 x 151936, 37 tiles per CU, 50.7 -> 42.9 us, and 62.5 -> 43.6
-// us at 4 tokens; at 2-3 tiles per CU it ties (Llama-7B gate/up) or loses
-// (configs[4] gate/up 9.0 -> 9.9 us), and with one tile per CU or fewer the
-// register-ring kernel is 1.5-3 us faster).
+// lm_head 2560 x 151936, 37 tiles per CU, 50.6 -> 42.0 us, and 62.5 -> 43.6
+// us at 4 tokens; at 2-3 tiles per CU it ties (Llama-7B gate/up 12.1 against
+// 12.3 us), and with one tile per CU or fewer the register-ring kernel is
+// 1-2 us faster: q_proj 4.9 against 6.7, down 8.6 against 9.5).
 constexpr int kStreamMinTilesCu = 8;
 
 // The streaming kernel when it is chosen and the call fits it, else the

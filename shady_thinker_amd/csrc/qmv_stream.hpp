@@ -17,7 +17,7 @@
 //    buffer-to-LDS DMA (buffer_load_dwordx4 ... lds). The DMAs do not depend
 //    on x, so ~96 KiB per CU are requested from the first cycles on, while x
 //    is loaded and staged.
-//  * The workgroup (one per CU, 16 waves) owns a contiguous run of tiles;
+//  * The workgroup (16 or 8 waves) owns a contiguous run of tiles;
 //    their units, flattened tile-major, are one contiguous byte range of the
 //    tiled layout. Wave w takes the w-th sixteenth of that range, so every
 //    wave streams the same number of units (no 3-versus-2-tile imbalance)
@@ -41,10 +41,13 @@
 namespace st {
 namespace qmv {
 
-constexpr int kStreamWaves = 16;
-constexpr int kStreamRingTarget = 96 * 1024;  // LDS ring bytes per workgroup (D is derived from it)
-constexpr int kStreamMaxRows = 2 * kStreamWaves;  // x staging: at most two 64-item rows per wave
+constexpr int kStreamRingPerWave = 6 * 1024;  // LDS ring bytes per wave (D is derived from it)
+constexpr int kStreamRows = 2;  // x staging: at most two 64-item rows per wave
 constexpr size_t kLdsBytes = 160 * 1024;
+#ifndef ST_STREAM_PRIO
+#define ST_STREAM_PRIO 1
+#endif
+constexpr bool kStreamPrio = ST_STREAM_PRIO;
 
 template <int FMT, int SPU>
 constexpr int stream_wpu() { return is_i8(FMT) ? 8 : 2 * SPU; }  // weight dwords per lane per unit
@@ -55,16 +58,16 @@ constexpr int stream_wd() {  // DMA instructions per unit and source
 template <int FMT, int NSRC, int SPU>
 constexpr int stream_depth() {
     constexpr int wb = 256 * stream_wpu<FMT, SPU>();
-    constexpr int d = kStreamRingTarget / (kStreamWaves * NSRC * wb);
+    constexpr int d = kStreamRingPerWave / (NSRC * wb);
     return d < 2 ? 2 : (d > 12 ? 12 : d);
 }
 template <int FMT, int NSRC, int SPU, bool HZ>
 constexpr int stream_lpu() {  // loads per unit: weight DMAs + scale (+ zero word); INT8: + its column scale
     return NSRC * (stream_wd<FMT, SPU>() + 1 + (HZ ? 1 : 0));
 }
-template <int FMT, int NSRC, int SPU>
+template <int FMT, int NSRC, int SPU, int NW>
 constexpr int stream_ring_bytes() {
-    return kStreamWaves * stream_depth<FMT, NSRC, SPU>() * NSRC * 256 * stream_wpu<FMT, SPU>();
+    return NW * stream_depth<FMT, NSRC, SPU>() * NSRC * 256 * stream_wpu<FMT, SPU>();
 }
 
 // s_waitcnt vmcnt(n) for a constant n < 64 (expcnt, lgkmcnt left at their maxima)
@@ -89,26 +92,30 @@ __device__ __forceinline__ void dma16(__amdgpu_buffer_rsrc_t r, unsigned char *l
 #ifdef ST_STREAM_TRACE
 __device__ unsigned long long st_stream_trace[2048 * 16 * 8];
 #define ST_TR(k) \
-    if (lane == 0) st_stream_trace[((size_t)blockIdx.x * 16 + wave) * 8 + (k)] = __builtin_amdgcn_s_memrealtime()
+    if (lane == 0 && blockIdx.x < 2048) \
+    st_stream_trace[((size_t)blockIdx.x * 16 + wave) * 8 + (k)] = __builtin_amdgcn_s_memrealtime()
 #else
 #define ST_TR(k)
 #endif
 
-template <int FMT, int NSRC, int XM, int SPU, bool PERM, bool HZ>
-__global__ __launch_bounds__(64 * kStreamWaves) void qmv_stream_kernel(Params p) {
-    constexpr int NW = kStreamWaves;
+template <int FMT, int NSRC, int XM, int SPU, bool PERM, bool HZ, int NW>
+__global__ __launch_bounds__(64 * NW) void qmv_stream_kernel(Params p) {
     constexpr int IPU = 4 * SPU;  // 16-k staging items per group and token
     constexpr int WPU = stream_wpu<FMT, SPU>();
-    constexpr int WB = 256 * WPU;  // bytes of one unit of one source
+    constexpr int WB = 256 * WPU;  // LDS bytes of one unit of one source (= its HBM bytes)
     constexpr int WD = stream_wd<FMT, SPU>();
     constexpr int D = stream_depth<FMT, NSRC, SPU>();
     constexpr int LPU = stream_lpu<FMT, NSRC, SPU, HZ>();
     static_assert(D * LPU < 64, "ring wait exceeds vmcnt");
-    constexpr int RMAX = kStreamMaxRows / NW;
-    __shared__ __align__(16) unsigned char ring[stream_ring_bytes<FMT, NSRC, SPU>()];
-    extern __shared__ __align__(16) unsigned char smem[];  // A operands, es, partial sums
+    constexpr int RMAX = kStreamRows;
+    __shared__ __align__(16) unsigned char ring[stream_ring_bytes<FMT, NSRC, SPU, NW>()];
+    extern __shared__ __align__(16) unsigned char smem[];  // A operands, es, a zero block, partial sums
 
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    // Everything indexed by the wave is uniform: the wave index is read into
+    // a scalar register, so the cursors below live in SGPRs and the per-unit
+    // bookkeeping is scalar work.
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int q = lane >> 4, c = lane & 15;
     const int M = p.M, N = p.N, G = p.units, RB = p.rb;
 
@@ -122,9 +129,12 @@ __global__ __launch_bounds__(64 * kStreamWaves) void qmv_stream_kernel(Params p)
     const int nu = ub - ua;
     ST_TR(0);
 
+    const int ASTEP = 4 * RB;                // u32x4 per (group, step) of A
+    const int AUNIT = SPU * ASTEP;           // u32x4 per group of A
     u32x4 *abuf = reinterpret_cast<u32x4 *>(smem);  // [group][step][q][row]
-    u32x4 *s_es = abuf + (size_t)G * SPU * 4 * RB;  // [group][token]
-    float *red = reinterpret_cast<float *>(s_es + (size_t)G * M);  // [wave][first, last][src][lane]
+    u32x4 *s_es = abuf + (size_t)G * AUNIT;  // [group][token]
+    u32x4 *zblk = s_es + (size_t)G * M;      // AUNIT zero records (the A operand of rows >= RB)
+    float *red = reinterpret_cast<float *>(zblk + AUNIT);  // [wave][first, last][src][lane]
 
     // ------------------------------------------------------------ staging
     // The first nrows waves stage x, 64 items (16 k of one group and token)
@@ -145,11 +155,17 @@ __global__ __launch_bounds__(64 * kStreamWaves) void qmv_stream_kernel(Params p)
     }
 
     // --------------------------------------------------------------- ring
-    const __amdgpu_buffer_rsrc_t rw0 =
-        __builtin_amdgcn_make_buffer_rsrc((void *)(is_i8(FMT) ? (const void *)p.w8 : (const void *)p.qw[0]), (short)0,
-                                          0x7FFFFFFF, kBufWord3);
-    const __amdgpu_buffer_rsrc_t rw1 =
-        __builtin_amdgcn_make_buffer_rsrc((void *)p.qw[NSRC - 1], (short)0, 0x7FFFFFFF, kBufWord3);
+    // Weights: one buffer resource per wave and source covering exactly the
+    // wave's units, so the ring's issues past the last unit are out of
+    // range (no memory access, still one load each): every unit issues the
+    // same LPU loads and the ring wait is a constant.
+    constexpr unsigned UB = 64u * WPU * 4u;  // HBM bytes of one unit of one source
+    const size_t wfirst = ((size_t)t0 * G + ua) * UB;
+    const unsigned wrange = (unsigned)nu * UB;
+    const char *wsrc0 = static_cast<const char *>(is_i8(FMT) ? (const void *)p.w8 : (const void *)p.qw[0]) + wfirst;
+    const char *wsrc1 = reinterpret_cast<const char *>(p.qw[NSRC - 1]) + wfirst;
+    const __amdgpu_buffer_rsrc_t rw0 = __builtin_amdgcn_make_buffer_rsrc((void *)wsrc0, (short)0, wrange, kBufWord3);
+    const __amdgpu_buffer_rsrc_t rw1 = __builtin_amdgcn_make_buffer_rsrc((void *)wsrc1, (short)0, wrange, kBufWord3);
     const __amdgpu_buffer_rsrc_t rs0 = __builtin_amdgcn_make_buffer_rsrc(
         (void *)(is_i8(FMT) ? (const void *)p.scale8 : (const void *)p.sc[0]), (short)0, 0x7FFFFFFF, kBufWord3);
     const __amdgpu_buffer_rsrc_t rs1 =
@@ -159,43 +175,50 @@ __global__ __launch_bounds__(64 * kStreamWaves) void qmv_stream_kernel(Params p)
         __builtin_amdgcn_make_buffer_rsrc((void *)p.qz[NSRC - 1], (short)0, 0x7FFFFFFF, kBufWord3);
 
     unsigned char *wring = ring + (size_t)wave * D * NSRC * WB;
+    const unsigned vlane_w = lane * (WPU >= 4 ? WPU * 4 : 8);  // per-lane part of a unit's weight offset
+    const unsigned vlane_s = c * (is_i8(FMT) ? 4u : 2u);      // ... of its scale
+    const unsigned vlane_z = (c >> 3) * 4u;                    // ... of its zero word
     unsigned meta[NSRC][D];  // scale bits (GPTQ: f16; INT8: the column's f32 scale)
     unsigned zw[NSRC][HZ ? D : 1];
-    // issue cursor: unit ua + i of the workgroup = tile t0 + it, group ig
+    // issue cursor (scalar): the unit's tile t0 + it, group ig, and the
+    // scalar byte offsets of its scales and zero words; past the wave's
+    // last unit the cursor stays there (those scale loads read a valid,
+    // cached address and are never used)
     int it = ua / max(G, 1), ig = ua - it * G;
+    unsigned soff = is_i8(FMT) ? (unsigned)(t0 + it) * 64u : ((unsigned)ig * N + (unsigned)(t0 + it) * 16u) * 2u;
+    unsigned zoff = ((unsigned)ig * (N >> 3) + (unsigned)(t0 + it) * 2u) * 4u;
     auto issue = [&](int i, int d) {  // unit i into ring slot d (d constant after unrolling)
-        const bool live = i < nu;
-        const int tile = t0 + it;
+        const unsigned vw = vlane_w + (unsigned)i * UB;
 #pragma unroll
         for (int src = 0; src < NSRC; ++src) {
             const __amdgpu_buffer_rsrc_t rw = src == 0 ? rw0 : rw1;
             unsigned char *dst = wring + (d * NSRC + src) * WB;
-            const unsigned base = (unsigned)(tile * G + ig) * (64u * WPU * 4u);
 #pragma unroll
             for (int j = 0; j < WD; ++j) {
-                if constexpr (WPU >= 4) {
-                    const unsigned off = live ? base + lane * (WPU * 4) + 16 * j : kNoLoad;
-                    dma16<ring_cache_policy<NSRC>>(rw, dst + 1024 * j, off);
-                } else {
-                    const unsigned off = live ? base + lane * 8 + 4 * j : kNoLoad;
+                if constexpr (WPU >= 4)
+                    dma16<ring_cache_policy<NSRC>>(rw, dst + 1024 * j, vw + 16 * j);
+                else
                     __builtin_amdgcn_raw_ptr_buffer_load_lds(rw, (__attribute__((address_space(3))) void *)(dst + 256 * j),
-                                                             4, off, 0, 0, ring_cache_policy<NSRC>);
-                }
+                                                             4, vw + 4 * j, 0, 0, ring_cache_policy<NSRC>);
             }
-            const int n = tile * kTileN + c;
             if constexpr (is_i8(FMT)) {
-                meta[src][d] = __builtin_amdgcn_raw_buffer_load_b32(rs0, live ? (unsigned)n * 4u : kNoLoad, 0, 0);
+                meta[src][d] = __builtin_amdgcn_raw_buffer_load_b32(rs0, vlane_s, soff, 0);
             } else {
-                meta[src][d] = __builtin_amdgcn_raw_buffer_load_b16(src == 0 ? rs0 : rs1,
-                                                                    live ? (unsigned)(ig * N + n) * 2u : kNoLoad, 0, 0);
-                if constexpr (HZ)
-                    zw[src][d] = __builtin_amdgcn_raw_buffer_load_b32(
-                        src == 0 ? rz0 : rz1, live ? (unsigned)(ig * (N >> 3) + (n >> 3)) * 4u : kNoLoad, 0, 0);
+                meta[src][d] = __builtin_amdgcn_raw_buffer_load_b16(src == 0 ? rs0 : rs1, vlane_s, soff, 0);
+                if constexpr (HZ) zw[src][d] = __builtin_amdgcn_raw_buffer_load_b32(src == 0 ? rz0 : rz1, vlane_z, zoff, 0);
             }
         }
-        if (++ig == G) {
-            ig = 0;
-            ++it;
+        if (i + 1 < nu) {
+            if constexpr (!is_i8(FMT)) {
+                soff += 2u * N;
+                zoff += 4u * (N >> 3);
+            }
+            if (++ig == G) {
+                ig = 0;
+                ++it;
+                soff = is_i8(FMT) ? (unsigned)(t0 + it) * 64u : (unsigned)(t0 + it) * 32u;
+                zoff = (unsigned)(t0 + it) * 8u;
+            }
         }
     };
 #pragma unroll
@@ -217,6 +240,8 @@ __global__ __launch_bounds__(64 * kStreamWaves) void qmv_stream_kernel(Params p)
                                            ii == 0 ? &s_es[u * M + m] : nullptr);
         }
     }
+    if (wave == 0)
+        for (int i = lane; i < AUNIT; i += 64) zblk[i] = u32x4{0, 0, 0, 0};
     ST_TR(2);
     // x staged (and this wave's LDS writes landed) in every wave; the DMAs stay in flight
     asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
@@ -226,7 +251,7 @@ __global__ __launch_bounds__(64 * kStreamWaves) void qmv_stream_kernel(Params p)
     float tot[NSRC];
 #pragma unroll
     for (int src = 0; src < NSRC; ++src) tot[src] = 0.0f;
-    const int zoff = p.zoff;
+    const int zoff8 = p.zoff;
     // y of one tile from the full sums (lane: token q, column c)
     auto write_y = [&](int tile, const float (&v)[NSRC], float s8) {
         const int n = tile * kTileN + c;
@@ -236,18 +261,28 @@ __global__ __launch_bounds__(64 * kStreamWaves) void qmv_stream_kernel(Params p)
         if constexpr (is_i8(FMT)) out *= s8;
         p.y[(size_t)q * N + n] = out;
     };
+    const auto lds_addr = [](const void *ptr) {
+        return (unsigned)(size_t)((__attribute__((address_space(3))) const unsigned char *)ptr);
+    };
+    // per-lane LDS addresses of the A operand (rows >= RB read the zero
+    // block, which does not advance) and of the group scalars, advanced by
+    // one add per unit
+    const bool arow = c < RB;
+    const unsigned a_lane0 = arow ? lds_addr(abuf + q * RB + c) : lds_addr(zblk);
+    const unsigned a_step = arow ? (unsigned)ASTEP * 16u : 0u;
+    const unsigned a_unit = arow ? (unsigned)AUNIT * 16u : 0u;
+    const unsigned e_lane0 = lds_addr(s_es + min(q, M - 1));
     int ct = ua / max(G, 1), cg = ua - ct * G;  // compute cursor (tile t0 + ct, group cg)
-    const u32x4 *alane = abuf + q * RB + c;
+    unsigned aaddr = a_lane0 + (unsigned)cg * a_unit;
+    unsigned eaddr = e_lane0 + (unsigned)(cg * M) * 16u;
     auto compute = [&](int i, int d) {  // unit i from ring slot d
         wait_vm<(D - 1) * LPU>();
-        // the ring words of both sources: issued together, one wait (tied to
-        // the values, so nothing uses them before it) after the A-operand and
-        // scale-record reads are issued too
+        // every LDS read of the unit, issued together; one wait (tied to the
+        // values, so nothing uses them before it)
         unsigned w[NSRC][WPU];
 #pragma unroll
         for (int src = 0; src < NSRC; ++src) {
-            const unsigned la = (unsigned)(size_t)((__attribute__((address_space(3))) unsigned char *)(wring +
-                                                                                                      (d * NSRC + src) * WB));
+            const unsigned la = lds_addr(wring + (d * NSRC + src) * WB);
             if constexpr (WPU == 2) {
                 asm volatile("ds_read_b32 %0, %2\n\tds_read_b32 %1, %2 offset:256"
                              : "=v"(w[src][0]), "=v"(w[src][1])
@@ -262,22 +297,25 @@ __global__ __launch_bounds__(64 * kStreamWaves) void qmv_stream_kernel(Params p)
                 }
             }
         }
-        v4i A[SPU];
+        u32x4 A[SPU], es;
 #pragma unroll
-        for (int st = 0; st < SPU; ++st) A[st] = __builtin_bit_cast(v4i, alane[(cg * SPU + st) * 4 * RB]);
-        const u32x4 es = s_es[cg * M + min(q, M - 1)];
+        for (int st = 0; st < SPU; ++st)
+            asm volatile("ds_read_b128 %0, %1" : "=v"(A[st]) : "v"(aaddr + (unsigned)st * a_step) : "memory");
+        asm volatile("ds_read_b128 %0, %1" : "=v"(es) : "v"(eaddr) : "memory");
         asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
 #pragma unroll
         for (int src = 0; src < NSRC; ++src)
 #pragma unroll
             for (int j = 0; j < WPU; ++j) asm volatile("" : "+v"(w[src][j]));
+#pragma unroll
+        for (int st = 0; st < SPU; ++st) asm volatile("" : "+v"(A[st]));
+        asm volatile("" : "+v"(es));
         v4i acc[NSRC];
 #pragma unroll
         for (int src = 0; src < NSRC; ++src) {
             acc[src] = v4i{0, 0, 0, 0};
 #pragma unroll
             for (int st = 0; st < SPU; ++st) {
-                const v4i Ast = c < RB ? A[st] : v4i{0, 0, 0, 0};
                 v4i Bf;
                 if constexpr (is_i8(FMT)) {
                     Bf = v4i{(int)w[src][4 * st], (int)w[src][4 * st + 1], (int)w[src][4 * st + 2], (int)w[src][4 * st + 3]};
@@ -286,7 +324,7 @@ __global__ __launch_bounds__(64 * kStreamWaves) void qmv_stream_kernel(Params p)
                     Bf = v4i{(int)(w0 & 0x0F0F0F0Fu), (int)((w0 >> 4) & 0x0F0F0F0Fu), (int)(w1 & 0x0F0F0F0Fu),
                              (int)((w1 >> 4) & 0x0F0F0F0Fu)};
                 }
-                acc[src] = __builtin_amdgcn_mfma_i32_16x16x64_i8(Ast, Bf, acc[src], 0, 0, 0);
+                acc[src] = __builtin_amdgcn_mfma_i32_16x16x64_i8(__builtin_bit_cast(v4i, A[st]), Bf, acc[src], 0, 0, 0);
             }
         }
         // group epilogue: exact sum(q X) - z sum(X) as hi 65536 + lo, one
@@ -300,15 +338,15 @@ __global__ __launch_bounds__(64 * kStreamWaves) void qmv_stream_kernel(Params p)
             int z = is_i8(FMT) ? 0 : 8;  // INT8 is symmetric; GPTQ without zero points: z = 8
             if constexpr (!is_i8(FMT)) {
                 f = (float)__builtin_bit_cast(_Float16, (unsigned short)meta[src][d]) * em;
-                if constexpr (HZ) z = (int)((zw[src][d] >> (4 * (c & 7))) & 0xF) + zoff;
+                if constexpr (HZ) z = (int)((zw[src][d] >> (4 * (c & 7))) & 0xF) + zoff8;
             }
             const int hi = S.x + __mul24(z, nh);
             const int lo = (S.y << 8) + S.z + __mul24(z, nl);
             tot[src] = fmaf(fmaf((float)hi, 65536.0f, (float)lo), f, tot[src]);
         }
-        // end of a tile, or of this wave's range: full tiles go out, partial
-        // ones to LDS (slot 0: the tile began before this range; slot 1: it
-        // began in it and runs on past it)
+        // end of a tile, or of this wave's range (a scalar test): full tiles
+        // go out, partial ones to LDS (slot 0: the tile began before this
+        // range; slot 1: it began in it and runs on past it)
         const int f = ua + i;
         if (cg == G - 1 || f == ub - 1) {
             const int ts = ct * G;
@@ -323,11 +361,22 @@ __global__ __launch_bounds__(64 * kStreamWaves) void qmv_stream_kernel(Params p)
 #pragma unroll
             for (int src = 0; src < NSRC; ++src) tot[src] = 0.0f;
         }
+        aaddr += a_unit;
+        eaddr += (unsigned)M * 16u;
         if (++cg == G) {
             cg = 0;
             ++ct;
+            aaddr = a_lane0;
+            eaddr = e_lane0;
         }
     };
+    // Issue priority follows the work left: the CU's memory queue is always
+    // full, and by default the oldest waves win every free slot, so they
+    // finish first and the youngest run the last part alone with a quarter
+    // of the loads in flight. A wave lowers its priority as its remaining
+    // share shrinks (quarters of its range), which keeps the waves level.
+    int prio = 3;
+    __builtin_amdgcn_s_setprio(3);
     for (int i0 = 0; i0 < nu; i0 += D) {
 #pragma unroll
         for (int d = 0; d < D; ++d) {
@@ -335,8 +384,16 @@ __global__ __launch_bounds__(64 * kStreamWaves) void qmv_stream_kernel(Params p)
             if (i0 + d == 0) ST_TR(7);
             issue(i0 + d + D, d);  // always: the count of loads per unit is fixed
         }
+        const int rem = nu - (i0 + D);  // units left after this block
+        const int tp = rem <= 0 ? 0 : min(3, rem * 4 / nu);
+        if (kStreamPrio && tp < prio) {
+            prio = tp;
+            if (prio == 2) __builtin_amdgcn_s_setprio(2);
+            else if (prio == 1) __builtin_amdgcn_s_setprio(1);
+            else __builtin_amdgcn_s_setprio(0);
+        }
     }
-
+    __builtin_amdgcn_s_setprio(0);
     ST_TR(4);
     // ------------------------------------------ tiles split across waves
     __syncthreads();
@@ -366,32 +423,46 @@ __global__ __launch_bounds__(64 * kStreamWaves) void qmv_stream_kernel(Params p)
     ST_TR(6);
 }
 
-// Launches the streaming kernel when the call fits it; returns -1 (nothing
-// launched) when it does not: the caller then takes the register-ring kernel.
-template <int FMT, int NSRC, int XM, int SPU, bool PERM>
-int launch_stream(st_context *ctx, Params &p) {
-    if (p.M > 4 || p.N % kTileN) return -1;
+// One launch shape of the streaming kernel; -1 (nothing launched) when the
+// call does not fit it.
+template <int FMT, int NSRC, int XM, int SPU, bool PERM, int NW>
+int launch_stream_nw(st_context *ctx, Params &p, int grid) {
     const int items = p.M * p.units * 4 * SPU;
-    if (items > 64 * kStreamMaxRows) return -1;
-    p.rb = 4 * p.M;
-    const size_t dyn = (size_t)p.units * SPU * 4 * p.rb * 16 + (size_t)p.units * p.M * 16 +
-                       (size_t)kStreamWaves * 2 * NSRC * 64 * sizeof(float);
-    if (dyn + stream_ring_bytes<FMT, NSRC, SPU>() > kLdsBytes) return -1;
-    // 32-bit buffer offsets (weights, scales, zero words)
-    if ((size_t)p.ntiles * kTileN * p.K / 2 * (is_i8(FMT) ? 2 : 1) >= (size_t(1) << 31)) return -1;
-    p.grid = std::min(std::max(1, ctx->num_cus), p.ntiles);
-    p.nwaves = kStreamWaves;
+    if (items > 64 * kStreamRows * NW) return -1;
+    const size_t dyn = (size_t)p.units * SPU * 4 * p.rb * 16 + (size_t)p.units * p.M * 16 + (size_t)SPU * 4 * p.rb * 16 +
+                       (size_t)NW * 2 * NSRC * 64 * sizeof(float);
+    if (dyn + stream_ring_bytes<FMT, NSRC, SPU, NW>() > kLdsBytes) return -1;
+    p.grid = grid;
+    p.nwaves = NW;
     const bool hz = !is_i8(FMT) && p.qz[0];
     if (!is_i8(FMT) && !p.qz[0] != !p.qz[NSRC - 1]) return -1;  // zero points on one source only
     auto go = [&](auto kern) -> int {
         ST_HIP(hipFuncSetAttribute((const void *)kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)dyn));
-        hipLaunchKernelGGL(kern, dim3(p.grid), dim3(64 * kStreamWaves), dyn, ctx->stream, p);
+        hipLaunchKernelGGL(kern, dim3(p.grid), dim3(64 * NW), dyn, ctx->stream, p);
         return launch_check("qmv_stream_kernel");
     };
     if constexpr (!is_i8(FMT)) {
-        if (hz) return go(qmv_stream_kernel<FMT, NSRC, XM, SPU, PERM, true>);
+        if (hz) return go(qmv_stream_kernel<FMT, NSRC, XM, SPU, PERM, true, NW>);
     }
-    return go(qmv_stream_kernel<FMT, NSRC, XM, SPU, PERM, false>);
+    return go(qmv_stream_kernel<FMT, NSRC, XM, SPU, PERM, false, NW>);
+}
+
+// Launches the streaming kernel when the call fits it; returns -1 (nothing
+// launched) when it does not: the caller then takes the register-ring kernel.
+// Shape: 16 waves per workgroup and one workgroup per CU unless the context
+// settings STREAM_WAVES (8 or 16) / STREAM_TILES_WG (tiles per workgroup)
+// say otherwise.
+template <int FMT, int NSRC, int XM, int SPU, bool PERM>
+int launch_stream(st_context *ctx, Params &p) {
+    if (p.M > 4 || p.N % kTileN) return -1;
+    // 32-bit buffer offsets (weights, scales, zero words)
+    if ((size_t)p.ntiles * kTileN * p.K / 2 * (is_i8(FMT) ? 2 : 1) >= (size_t(1) << 31)) return -1;
+    p.rb = 4 * p.M;
+    const int ncu = std::max(1, ctx->num_cus);
+    const int tpw = tune(ctx, ST_TUNE_STREAM_TILES_WG, 0);
+    const int grid = std::min(p.ntiles, tpw > 0 ? (p.ntiles + tpw - 1) / tpw : ncu);
+    if (tune(ctx, ST_TUNE_STREAM_WAVES, 16) == 8) return launch_stream_nw<FMT, NSRC, XM, SPU, PERM, 8>(ctx, p, grid);
+    return launch_stream_nw<FMT, NSRC, XM, SPU, PERM, 16>(ctx, p, grid);
 }
 
 }  // namespace qmv
