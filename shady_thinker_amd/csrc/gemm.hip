@@ -42,6 +42,7 @@ namespace {
 typedef _Float16 half2_t __attribute__((ext_vector_type(2)));
 typedef _Float16 half8 __attribute__((ext_vector_type(8)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef float f32x8 __attribute__((ext_vector_type(8)));
 typedef unsigned u32x4 __attribute__((ext_vector_type(4)));
 typedef unsigned u32x2 __attribute__((ext_vector_type(2)));
 
@@ -100,8 +101,8 @@ __device__ __forceinline__ half8 word_to_b(unsigned w, const BConv &c) {
 template <int GS, bool TILED, bool F16OUT, int CB_>
 __global__ __launch_bounds__(kThreads, kWavesPerSimd) void gemm_kernel(const _Float16 *__restrict__ A, const uint32_t *__restrict__ qw,
                                                            const uint16_t *__restrict__ sc, const uint32_t *__restrict__ qz,
-                                                           int zoff, void *__restrict__ C, int M, int K, int N,
-                                                           int kps, float *__restrict__ part) {
+                                                           int zoff, const float *__restrict__ rsc, void *__restrict__ C,
+                                                           int M, int K, int N, int kps, float *__restrict__ part) {
     constexpr int CB = CB_;            // (hides the namespace-scope defaults)
     constexpr int BN = 32 * CB * WN;
     // Two separate arrays (not one [2][...]) so that alias analysis can tell
@@ -347,12 +348,14 @@ __global__ __launch_bounds__(kThreads, kWavesPerSimd) void gemm_kernel(const _Fl
             for (int i = 0; i < 16; ++i) {
                 const int m = m0 + mw + rb * 32 + 8 * (i >> 2) + 4 * hi + (i & 3);
                 if (m >= M) continue;
+                // rows the pre-pass scaled down by 2^-e get 2^e back (exact)
+                const float v = rsc ? acc[rb][cb][i] * rsc[m] : acc[rb][cb][i];
                 if (part)  // split-K: this split's f32 partial
-                    part[((size_t)split * M + m) * N + n] = acc[rb][cb][i];
+                    part[((size_t)split * M + m) * N + n] = v;
                 else if constexpr (F16OUT)
-                    static_cast<_Float16 *>(C)[(size_t)m * N + n] = (_Float16)acc[rb][cb][i];
+                    static_cast<_Float16 *>(C)[(size_t)m * N + n] = (_Float16)v;
                 else
-                    static_cast<float *>(C)[(size_t)m * N + n] = acc[rb][cb][i];
+                    static_cast<float *>(C)[(size_t)m * N + n] = v;
             }
         }
 }
@@ -377,19 +380,49 @@ __device__ __forceinline__ u32x4 to_b_order(u32x4 a) {
 // (src/model.rs:803-811) for a block of tokens.
 __global__ __launch_bounds__(256) void prep_a_kernel(const _Float16 *__restrict__ A, const _Float16 *__restrict__ U,
                                                      const int32_t *__restrict__ perm, _Float16 *__restrict__ out,
-                                                     int K) {
+                                                     float *__restrict__ rsc, int K) {
     extern __shared__ _Float16 row[];
+    __shared__ unsigned s_hmax;
     const size_t base = (size_t)blockIdx.x * K;
+    auto silu_mul = [&](int k) {
+        const half8 g = *reinterpret_cast<const half8 *>(A + base + k);
+        const half8 u = *reinterpret_cast<const half8 *>(U + base + k);
+        float h[8];
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+            const float gv = (float)g[e];
+            h[e] = __fdividef(gv, 1.0f + __expf(-gv)) * (float)u[e];
+        }
+        return *reinterpret_cast<const f32x8 *>(h);
+    };
+    // silu(g) * u can exceed the f16 range (65504) although g and u are f16:
+    // a row whose largest |h| is 2^15 or more is stored as h * 2^-e (e so
+    // that it lies in [2^14, 2^15)) and the GEMM multiplies its row of C by
+    // 2^e (rsc); other rows keep e = 0. Non-finite h is left as it is.
+    float inv = 1.0f;
+    if (U) {
+        if (threadIdx.x == 0) s_hmax = 0;
+        __syncthreads();
+        float hm = 0.0f;
+        for (int k = threadIdx.x * 8; k < K; k += 256 * 8) {
+            const f32x8 h = silu_mul(k);
+#pragma unroll
+            for (int e = 0; e < 8; ++e) hm = fmaxf(hm, fabsf(h[e]));
+        }
+        atomicMax(&s_hmax, __float_as_uint(hm));  // non-negative floats order as their bits
+        __syncthreads();
+        const float hmax = __uint_as_float(s_hmax);
+        int e = 0;
+        if (hmax >= 32768.0f && hmax <= 3.4e38f) e = __builtin_amdgcn_frexp_expf(hmax) - 15;
+        inv = __builtin_amdgcn_ldexpf(1.0f, -e);
+        if (threadIdx.x == 0) rsc[blockIdx.x] = __builtin_amdgcn_ldexpf(1.0f, e);
+    }
     for (int k = threadIdx.x * 8; k < K; k += 256 * 8) {
         if (U) {
-            const half8 g = *reinterpret_cast<const half8 *>(A + base + k);
-            const half8 u = *reinterpret_cast<const half8 *>(U + base + k);
+            const f32x8 hv = silu_mul(k);
             half8 h;
 #pragma unroll
-            for (int e = 0; e < 8; ++e) {
-                const float gv = (float)g[e];
-                h[e] = (_Float16)(__fdividef(gv, 1.0f + __expf(-gv)) * (float)u[e]);
-            }
+            for (int e = 0; e < 8; ++e) h[e] = (_Float16)(hv[e] * inv);
             *reinterpret_cast<half8 *>(&row[k]) = h;
         } else {
             *reinterpret_cast<u32x4 *>(&row[k]) = *reinterpret_cast<const u32x4 *>(A + base + k);
@@ -445,23 +478,23 @@ struct Split {
 
 template <int GS, bool TILED, int CBL>
 int launch_cb(st_context *ctx, const _Float16 *A, const uint32_t *qw, const uint16_t *sc, const uint32_t *qz, int zoff,
-              void *C, bool f16out, int M, int K, int N, const Split &sp) {
+              const float *rsc, void *C, bool f16out, int M, int K, int N, const Split &sp) {
     const int T = ((M + BM - 1) / BM) * ((N + 32 * CBL * WN - 1) / (32 * CBL * WN));
     const dim3 grid(T * sp.S);
     if (f16out)
         hipLaunchKernelGGL((gemm_kernel<GS, TILED, true, CBL>), grid, dim3(kThreads), 0, ctx->stream, A, qw, sc, qz, zoff,
-                           C, M, K, N, sp.kps, sp.part);
+                           rsc, C, M, K, N, sp.kps, sp.part);
     else
         hipLaunchKernelGGL((gemm_kernel<GS, TILED, false, CBL>), grid, dim3(kThreads), 0, ctx->stream, A, qw, sc, qz, zoff,
-                           C, M, K, N, sp.kps, sp.part);
+                           rsc, C, M, K, N, sp.kps, sp.part);
     return st::launch_check("gemm_kernel");
 }
 
 template <int GS, bool TILED>
 int launch_gs(st_context *ctx, const _Float16 *A, const uint32_t *qw, const uint16_t *sc, const uint32_t *qz, int zoff,
-              void *C, bool f16out, int M, int K, int N, int cb, const Split &sp) {
-    const int rc = cb == 1 ? launch_cb<GS, TILED, 1>(ctx, A, qw, sc, qz, zoff, C, f16out, M, K, N, sp)
-                           : launch_cb<GS, TILED, 2>(ctx, A, qw, sc, qz, zoff, C, f16out, M, K, N, sp);
+              const float *rsc, void *C, bool f16out, int M, int K, int N, int cb, const Split &sp) {
+    const int rc = cb == 1 ? launch_cb<GS, TILED, 1>(ctx, A, qw, sc, qz, zoff, rsc, C, f16out, M, K, N, sp)
+                           : launch_cb<GS, TILED, 2>(ctx, A, qw, sc, qz, zoff, rsc, C, f16out, M, K, N, sp);
     if (rc) return rc;
     if (sp.S > 1) {
         const size_t MN = (size_t)M * N;
@@ -477,11 +510,11 @@ int launch_gs(st_context *ctx, const _Float16 *A, const uint32_t *qw, const uint
 
 template <bool TILED>
 int launch_tiled(st_context *ctx, const _Float16 *A, const uint32_t *qw, const uint16_t *sc, const uint32_t *qz, int zoff,
-                 void *C, bool f16out, int M, int K, int N, int gs, int cb, const Split &sp) {
+                 const float *rsc, void *C, bool f16out, int M, int K, int N, int gs, int cb, const Split &sp) {
     switch (gs) {
-        case 64: return launch_gs<64, TILED>(ctx, A, qw, sc, qz, zoff, C, f16out, M, K, N, cb, sp);
-        case 128: return launch_gs<128, TILED>(ctx, A, qw, sc, qz, zoff, C, f16out, M, K, N, cb, sp);
-        default: return launch_gs<256, TILED>(ctx, A, qw, sc, qz, zoff, C, f16out, M, K, N, cb, sp);
+        case 64: return launch_gs<64, TILED>(ctx, A, qw, sc, qz, zoff, rsc, C, f16out, M, K, N, cb, sp);
+        case 128: return launch_gs<128, TILED>(ctx, A, qw, sc, qz, zoff, rsc, C, f16out, M, K, N, cb, sp);
+        default: return launch_gs<256, TILED>(ctx, A, qw, sc, qz, zoff, rsc, C, f16out, M, K, N, cb, sp);
     }
 }
 
@@ -540,22 +573,26 @@ int gemm_impl(const char *fn, st_context *ctx, const uint16_t *a, const uint16_t
         return st::fail(ST_ERR_SHAPE, "%s: A or qweight above 2 GiB (M=%d K=%d N=%d); split M or N", fn, M,
                         K, N);
     if (K > 32768) return st::fail(ST_ERR_SHAPE, "%s: K=%d above 32768", fn, K);
-    const size_t need = (size_t)M * K * sizeof(_Float16);
+    // workspace: A' (M K halves), then (silu only) one f32 row scale per row
+    const size_t a_bytes = (size_t)M * K * sizeof(_Float16);
+    const size_t rsc_off = (a_bytes + 255) & ~size_t(255);
+    const size_t need = u ? rsc_off + (size_t)M * sizeof(float) : a_bytes;
     if (need > ctx->ws_bytes)
         return st::fail(ST_ERR_WORKSPACE, "%s: needs %zu B of workspace for A (st_context_reserve_workspace)", fn,
                         need);
     if (perm && !st::aligned16(perm)) return st::fail(ST_ERR_ALIGN, "%s: perm must be 16-byte aligned", fn);
     _Float16 *A = reinterpret_cast<_Float16 *>(ctx->ws);
+    float *rsc = u ? reinterpret_cast<float *>(reinterpret_cast<char *>(ctx->ws) + rsc_off) : nullptr;
     hipLaunchKernelGGL(prep_a_kernel, dim3(M), dim3(256), (size_t)K * sizeof(_Float16), ctx->stream,
-                       reinterpret_cast<const _Float16 *>(a), reinterpret_cast<const _Float16 *>(u), perm, A, K);
+                       reinterpret_cast<const _Float16 *>(a), reinterpret_cast<const _Float16 *>(u), perm, A, rsc, K);
     if (int rc = st::launch_check("prep_a_kernel")) return rc;
     const int zoff = (flags & ST_FLAG_ZEROS_PLUS_ONE) ? 1 : 0;
     const bool f16out = c_dtype == ST_F16;
     const int cb = pick_cb(ctx, M, N);
     const Split sp = plan_split(ctx, M, K, N, cb, need);
     if (flags & ST_FLAG_TILED)
-        return launch_tiled<true>(ctx, A, qweight, scales, qzeros, zoff, c, f16out, M, K, N, group_size, cb, sp);
-    return launch_tiled<false>(ctx, A, qweight, scales, qzeros, zoff, c, f16out, M, K, N, group_size, cb, sp);
+        return launch_tiled<true>(ctx, A, qweight, scales, qzeros, zoff, rsc, c, f16out, M, K, N, group_size, cb, sp);
+    return launch_tiled<false>(ctx, A, qweight, scales, qzeros, zoff, rsc, c, f16out, M, K, N, group_size, cb, sp);
 }
 
 }  // namespace

@@ -49,6 +49,37 @@ def test_silu_gemm(gpu, orc, Mr, K, N, gs, zeros, act, tiled):
         assert e < TOL_GEMM
 
 
+@pytest.mark.parametrize("split", [False, True])
+def test_silu_gemm_beyond_f16_range(gpu, orc, tune, split):
+    """silu(g) * u above the f16 maximum (g, u up to 6e4: h up to 3.6e9; the
+    A operand is f16): those rows are scaled by a power of two in the
+    pre-pass and scaled back on C, so C stays finite and within the bar of
+    the f64 oracle (every row separately: small-range rows beside them are
+    unaffected), with and without split-K (partials carry the scale)."""
+    K, N, gs = 1024, 264, 128
+    c = orc.gptq_case(62, K, N, gs, zeros=True)
+    w = up(gpu, c, True)
+    rng = np.random.default_rng(5)
+    g = rng.standard_normal((40, K)).astype(np.float32)
+    u = rng.standard_normal((40, K)).astype(np.float32)
+    g[1], u[1] = g[1] * 300, u[1] * 300          # |h| around 1e5: past 65504
+    g[2, :16], u[2, :16] = 60000.0, -60000.0      # a few h of -3.6e9
+    g[3] = np.minimum(np.abs(g[3]) * 2e4, 6e4)     # every h large (g stays a finite f16)
+    g, u = g.astype(np.float16), u.astype(np.float16)
+    want = ref(orc, orc.silu_gate_f64(g, u), c)
+    if not split:
+        tune(GEMM_NO_SPLIT=1)
+    y = torch.empty(40, N, device="cuda")
+    M.fused_silu_gptq_gemm(gpu, torch.from_numpy(g).cuda(), torch.from_numpy(u).cuda(), w.qweight, w.scales, y, K, N,
+                           gs, w.qzeros, w.perm, w.flags)
+    torch.cuda.synchronize()
+    y = y.cpu().numpy()
+    assert np.isfinite(y).all()
+    for r in range(40):
+        e = orc.rel_l2(y[r], want[r])
+        assert e < TOL_GEMM, (r, e)
+
+
 def test_silu_gemm_zero_gate(gpu, orc):
     """silu(0) = 0: a zero gate gives C = 0 exactly whatever up holds."""
     K, N, Mr = 512, 72, 48
