@@ -76,8 +76,9 @@ inline int launch_check(const char *what) {
 // (st_int8_matvec) has checked the arguments.
 int int8_mm_f16(st_context *ctx, const void *x, const int8_t *w, const float *scale, float *y, int M, int K, int N);
 // Multi-token GPTQ int4 matvec / gate-up on f16 MFMA (i4mm.hip), tiled
-// weights without act-order, M <= 16; checked by the caller.
-int int4_mm_f16(st_context *ctx, const void *x, bool x_f32, const uint32_t *const qw[2], const uint16_t *const sc[2],
-                const uint32_t *const qz[2], int zoff, float *y, int M, int K, int N, int gs, int nsrc);
+// weights (act-order through perm, or NULL), M <= 16; checked by the caller.
+int int4_mm_f16(st_context *ctx, const void *x, bool x_f32, const int32_t *perm, const uint32_t *const qw[2],
+                const uint16_t *const sc[2], const uint32_t *const qz[2], int zoff, float *y, int M, int K, int N,
+                int gs, int nsrc);
 
 }  // namespace st

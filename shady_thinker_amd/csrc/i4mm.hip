@@ -105,15 +105,20 @@ struct Unit {  // what a wave loads for one 128-k unit of its tile and source
 // 2^e of each (token, 128-k unit) in pe [M, K / 128]: x 2^-e = hi + lo with
 // |x 2^-e| < 1 over the unit. Every 8 k are stored in the B order of
 // word_to_b. One 16-lane DPP row per (token, unit), 8 k per lane.
-__global__ __launch_bounds__(256) void i4mm_prep_kernel(const float *__restrict__ x, _Float16 *__restrict__ xp,
-                                                        float *__restrict__ pe, int M, int K) {
+__global__ __launch_bounds__(256) void i4mm_prep_kernel(const float *__restrict__ x, const int32_t *__restrict__ perm,
+                                                        _Float16 *__restrict__ xp, float *__restrict__ pe, int M, int K) {
     const int units = K / 128;
     const int gid = blockIdx.x * 16 + (threadIdx.x >> 4), l = threadIdx.x & 15;
     const bool ok = gid < M * units;  // every lane runs the DPP max below
     const int t = ok ? gid / units : 0, u = ok ? gid % units : 0;
     const size_t k = (size_t)u * 128 + 8 * l;
     f32x4 a = {0.f, 0.f, 0.f, 0.f}, b = a;
-    if (ok) {
+    if (ok && perm) {  // act-order: k of the sorted weight rows reads x[perm[k]]
+        const int4 p0 = *reinterpret_cast<const int4 *>(perm + k), p1 = *reinterpret_cast<const int4 *>(perm + k + 4);
+        const float *xr = x + (size_t)t * K;
+        a = f32x4{xr[p0.x], xr[p0.y], xr[p0.z], xr[p0.w]};
+        b = f32x4{xr[p1.x], xr[p1.y], xr[p1.z], xr[p1.w]};
+    } else if (ok) {
         a = *reinterpret_cast<const f32x4 *>(x + (size_t)t * K + k);
         b = *reinterpret_cast<const f32x4 *>(x + (size_t)t * K + k + 4);
     }
@@ -394,6 +399,20 @@ int launch_gs(st_context *ctx, const void *x, const float *pe, const uint32_t *c
     return st::launch_check("i4mm_kernel");
 }
 
+// Act-order with f16 x: xg[t, k] = x[t, perm[k]] (the sorted weight rows'
+// order), 8 k per thread, into the workspace.
+__global__ __launch_bounds__(256) void i4mm_gather_kernel(const uint16_t *__restrict__ x, const int32_t *__restrict__ perm,
+                                                          uint16_t *__restrict__ xg, int M, int K) {
+    const size_t i = ((size_t)blockIdx.x * 256 + threadIdx.x) * 8;
+    if (i >= (size_t)M * K) return;
+    const size_t t = i / K, k = i % K;
+    const int4 p0 = *reinterpret_cast<const int4 *>(perm + k), p1 = *reinterpret_cast<const int4 *>(perm + k + 4);
+    const uint16_t *xr = x + t * K;
+    const u32x4 v = {xr[p0.x] | ((unsigned)xr[p0.y] << 16), xr[p0.z] | ((unsigned)xr[p0.w] << 16),
+                     xr[p1.x] | ((unsigned)xr[p1.y] << 16), xr[p1.z] | ((unsigned)xr[p1.w] << 16)};
+    *reinterpret_cast<u32x4 *>(xg + i) = v;
+}
+
 template <bool F32X, int NSRC, int MB>
 int launch_mb(st_context *ctx, const void *x, const float *pe, const uint32_t *const *qw, const uint16_t *const *sc,
               const uint32_t *const *qz, int zoff, float *y, int M, int K, int N, int gs, int ntiles, int G, int wpt) {
@@ -417,11 +436,13 @@ int launch_src(st_context *ctx, const void *x, const float *pe, const uint32_t *
 
 namespace st {
 
-// Arguments are checked by the entry points (tiled weights, no act-order,
-// M <= 16, K % 128 == 0, K % group_size == 0, N % 8 == 0, alignment, 32-bit
-// offsets).
-int int4_mm_f16(st_context *ctx, const void *x, bool x_f32, const uint32_t *const qw[2], const uint16_t *const sc[2],
-                const uint32_t *const qz[2], int zoff, float *y, int M, int K, int N, int gs, int nsrc) {
+// Arguments are checked by the entry points (tiled weights, M <= 16, K %
+// 128 == 0, K % group_size == 0, N % 8 == 0, alignment, 32-bit offsets).
+// perm (act-order, may be NULL): x is read as x[:, perm[k]], by the f32
+// pre-pass or, for f16 x, by a gather pass into the workspace.
+int int4_mm_f16(st_context *ctx, const void *x, bool x_f32, const int32_t *perm, const uint32_t *const qw[2],
+                const uint16_t *const sc[2], const uint32_t *const qz[2], int zoff, float *y, int M, int K, int N,
+                int gs, int nsrc) {
     const int ntiles = (N + kTileN - 1) / kTileN;
     const int maxt = kMaxTilesPerWg / nsrc;  // tiles per workgroup: each tile (and source) keeps >= 2 waves
     const int G = std::max(std::min(ctx->num_cus, ntiles), (ntiles + maxt - 1) / maxt);
@@ -439,9 +460,17 @@ int int4_mm_f16(st_context *ctx, const void *x, bool x_f32, const uint32_t *cons
         pe = reinterpret_cast<const float *>(reinterpret_cast<const char *>(ctx->ws) + xbytes);
         const int groups = M * (K / 128);
         hipLaunchKernelGGL(i4mm_prep_kernel, dim3((groups + 15) / 16), dim3(256), 0, ctx->stream,
-                           static_cast<const float *>(x), xp, const_cast<float *>(pe), M, K);
+                           static_cast<const float *>(x), perm, xp, const_cast<float *>(pe), M, K);
         if (int rc = launch_check("i4mm_prep_kernel")) return rc;
         xa = xp;
+    } else if (perm) {
+        const size_t xbytes = (size_t)M * K * 2;
+        if (!ctx->ws || xbytes > ctx->ws_bytes) return fail(ST_ERR_WORKSPACE, "int4_mm_f16: workspace below %zu B", xbytes);
+        uint16_t *xg = reinterpret_cast<uint16_t *>(ctx->ws);
+        hipLaunchKernelGGL(i4mm_gather_kernel, dim3((unsigned)(((size_t)M * K / 8 + 255) / 256)), dim3(256), 0,
+                           ctx->stream, static_cast<const uint16_t *>(x), perm, xg, M, K);
+        if (int rc = launch_check("i4mm_gather_kernel")) return rc;
+        xa = xg;
     }
     if (nsrc == 2)
         return x_f32 ? launch_src<true, 2>(ctx, xa, pe, qw, sc, qz, zoff, y, M, K, N, gs, ntiles, G, wpt)

@@ -66,8 +66,8 @@ __global__ __launch_bounds__(256) void repack8_kernel(const int8_t *__restrict__
     reinterpret_cast<uint4 *>(out)[idx] = *reinterpret_cast<const uint4 *>(w + (size_t)n * K + k0);
 }
 
-// The GPTQ entry points take the f16-MFMA kernel (tiled weights, no
-// act-order, f32 or f16 x) from this many tokens on, when N has more
+// The GPTQ entry points take the f16-MFMA kernel (tiled weights, with or
+// without act-order, f32 or f16 x) from this many tokens on, when N has more
 // 16-column tiles than the GPU has CUs (as measured on configs[4]'s shapes:
 // at 16 tokens q|k|v 12.0 -> 10.7 us, gate/up 20.2 -> 17.4, lm_head 134 -> 75;
 // with fewer tiles or tokens the integer-limb kernels are faster).
@@ -77,13 +77,14 @@ bool use_i4mm(const st_context *ctx, const QmvParams &p, bool tiled, int xm) {
     const int ntiles = (p.N + kTileN - 1) / kTileN;
     const int min_m = std::max(2, st::tune(ctx, ST_TUNE_I4MM_MIN_M, kI4mmMinM));
     const int min_tiles = st::tune(ctx, ST_TUNE_I4MM_MIN_TILES, ctx->num_cus + 1);
-    return tiled && !p.perm && (xm == XM_F32 || xm == XM_F16) && p.M <= 16 && p.M >= min_m && ntiles >= min_tiles &&
+    return tiled && (xm == XM_F32 || xm == XM_F16) && p.M <= 16 && p.M >= min_m && ntiles >= min_tiles &&
            p.K % 128 == 0 && (size_t)ntiles * kTileN * p.K / 2 < (size_t(1) << 31);
 }
 
 int launch_i4(st_context *ctx, QmvParams &p, bool tiled, int nsrc, int xm) {
     if (use_i4mm(ctx, p, tiled, xm))
-        return st::int4_mm_f16(ctx, p.x, xm == XM_F32, p.qw, p.sc, p.qz, p.zoff, p.y, p.M, p.K, p.N, p.gs, nsrc);
+        return st::int4_mm_f16(ctx, p.x, xm == XM_F32, p.perm, p.qw, p.sc, p.qz, p.zoff, p.y, p.M, p.K, p.N, p.gs,
+                               nsrc);
     p.units = p.K / p.gs;
     p.ntiles = (p.N + kTileN - 1) / kTileN;
     // the tiled kernels address the weights with 32-bit buffer offsets
@@ -166,11 +167,13 @@ int st_gptq_i4_matvec_noalloc(st_context *ctx, const void *x, int x_dtype, const
     if (!ctx) return st::fail(ST_ERR_INVALID, "st_gptq_i4_matvec_noalloc: ctx is NULL");
     if (!ctx->scratch) return st::fail(ST_ERR_WORKSPACE, "st_gptq_i4_matvec_noalloc: no scratch on this device");
     // The most any path of the call keeps: the f16-MFMA kernel's split of one
-    // 16-token block of f32 x (2 f16 rows per token and a factor per 128 k);
-    // split-K partials shrink (or go unsplit) to fit what is there.
-    if (M > 0 && K > 0 && x_dtype == ST_F32) {
+    // 16-token block of f32 x (2 f16 rows per token and a factor per 128 k)
+    // or, for f16 x under act-order, its gathered rows; split-K partials
+    // shrink (or go unsplit) to fit what is there.
+    if (M > 0 && K > 0 && (x_dtype == ST_F32 || perm)) {
+        // (f16 x under act-order: the gathered rows, mb K halves)
         const size_t mb = (size_t)std::min(M, kTokenBlock);
-        const size_t need = 2 * mb * K * 2 + mb * (size_t)(K / 128) * 4;
+        const size_t need = x_dtype == ST_F32 ? 2 * mb * K * 2 + mb * (size_t)(K / 128) * 4 : mb * K * 2;
         if (need > ST_NOALLOC_SCRATCH_BYTES)
             return st::fail(ST_ERR_WORKSPACE, "st_gptq_i4_matvec_noalloc: %zu bytes of scratch needed, %u held", need,
                             (unsigned)ST_NOALLOC_SCRATCH_BYTES);

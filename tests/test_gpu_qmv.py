@@ -742,7 +742,7 @@ def _gate_up(gpu, wg, wu, x, dtype=torch.float32):
         xt = xt.half()
     y = torch.empty(x.shape[0], wg.N, device=gpu.device)
     M.fused_gate_up_silu(gpu, xt, wg.qweight, wg.scales, wu.qweight, wu.scales, y, wg.K, wg.N, wg.group_size,
-                         gate_qz=wg.qzeros, up_qz=wu.qzeros, flags=wg.flags)
+                         gate_qz=wg.qzeros, up_qz=wu.qzeros, perm=wg.perm, flags=wg.flags)
     torch.cuda.synchronize()
     return y.cpu().numpy()
 
@@ -781,6 +781,41 @@ def test_int4_mm_f16(gpu, orc, Mr, K, N, gs, zeros, f16, dual, tune):
     y = run()
     e = orc.rel_l2(y, ref)
     print(f"int4 f16-MFMA M={Mr} K={K} N={N} gs={gs} dual={dual} rel-L2 {e:.3e}")
+    assert np.isfinite(y).all() and e < 1e-5
+    tune(I4MM_MIN_M=99)
+    assert orc.rel_l2(run(), ref) < TOL
+
+
+@pytest.mark.parametrize("Mr,K,N,gs,zeros,f16,dual", [
+    (16, 2560, 6144, 128, False, False, False),  # configs[4] q|k|v shape, f32 x (gathered in the pre-pass)
+    (12, 1024, 4112, 64, True, True, False),     # f16 x (gather pass), zeros, group 64, 257 tiles
+    (16, 2560, 9728, 128, True, False, True),    # gate/up, f32 x
+    (13, 1536, 5200, 256, False, True, True),    # gate/up, f16 x, group 256
+])
+def test_int4_mm_f16_act_order(gpu, orc, Mr, K, N, gs, zeros, f16, dual, tune):
+    """Act-order checkpoints on the f16-MFMA kernel (12-16 tokens): x read
+    through the upload's permutation (rows sorted by group), against the f64
+    oracle with scale[g_idx[k]], and against the integer-limb kernels."""
+    _force_i4mm(tune)
+    xd = np.float16 if f16 else np.float32
+    c = orc.gptq_case(170 + Mr, K, N, gs, zeros=zeros, act_order=True, M=Mr, x_dtype=xd)
+    w = up(gpu, c)
+    assert w.perm is not None
+    dt = torch.float16 if f16 else torch.float32
+    f64 = lambda cc: orc.gptq_matvec_f64(c["x"], cc["qweight"], cc["scales"], K, N, gs, qzeros=cc["qzeros"],
+                                         g_idx=c["g_idx"])
+    ref = f64(c)
+    if dual:
+        c2 = orc.gptq_case(270 + Mr, K, N, gs, zeros=zeros)
+        c2["g_idx"] = c["g_idx"]
+        w2 = up(gpu, c2)
+        ref = orc.silu_gate_f64(ref, f64(c2))
+        run = lambda: _gate_up(gpu, w, w2, c["x"], dt)
+    else:
+        run = lambda: run_matvec(gpu, w, c["x"], dt)
+    y = run()
+    e = orc.rel_l2(y, ref)
+    print(f"int4 f16-MFMA act-order M={Mr} K={K} N={N} gs={gs} dual={dual} rel-L2 {e:.3e}")
     assert np.isfinite(y).all() and e < 1e-5
     tune(I4MM_MIN_M=99)
     assert orc.rel_l2(run(), ref) < TOL
