@@ -195,7 +195,9 @@ def main():
     ap.add_argument("--no-stack", action="store_true", help="skip the configs[4] 36-layer linear stack")
     ap.add_argument("--copy-calibrate", action="store_true",
                     help="profiling helper: 10 plain 64 MiB device copies (calibrates FETCH_SIZE / WRITE_SIZE)")
-    ap.add_argument("--only", default="", help="profiling helper: launch only this kernel, eagerly (q|gate_up|down|gemm|gemm512)")
+    ap.add_argument("--only", default="", help="profiling helper: launch only this kernel, eagerly "
+                                               "(q|gate_up|down|gemm|gemm512|lm_int4), or replay one configs[4] "
+                                               "stack step per step (stack1|stack16)")
     args = ap.parse_args()
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:
@@ -233,6 +235,20 @@ def main():
                        args.steps, args.warmup)
         print(json.dumps({"only": args.only, "M": Mr, "steps": args.steps, "ms_eager": round(ms, 5),
                           "TFLOP/s": round(2.0 * Mr * K * N / (ms * 1e-3) / 1e12, 1)}))
+        return
+
+    if args.only == "lm_int4":  # eager int4 lm_head calls, 4 cold copies (for the profiler)
+        K, N = 2560, 151936
+        W = [make_gptq(torch, dev, K, N, gen, gpu) for _ in range(4)]
+        x = torch.randn(1, K, device=dev, generator=gen)
+        y = torch.empty(1, N, device=dev)
+        ms = time_loop(torch, lambda i: Mdl.gptq_matvec(gpu, "lm_head", x, W[i % 4][0], W[i % 4][1], y, K, N, GS,
+                                                        flags=sta._lib.ST_FLAG_TILED), args.steps, args.warmup)
+        print(json.dumps({"only": args.only, "steps": args.steps, "ms_eager": round(ms, 5)}))
+        return
+    if args.only in ("stack1", "stack16"):  # configs[4] stack: graph replays (per-linear kernel times in the profile)
+        out = bench_stack(torch, dev, gpu, Mdl, gen, args, batches=(int(args.only[5:]),), prefill=False)
+        print(json.dumps({"only": args.only, **out}))
         return
 
     H, I = 4096, 11008
@@ -373,7 +389,7 @@ def bench_gemm(torch, dev, gpu, Mdl, gen, args):
     return out
 
 
-def bench_stack(torch, dev, gpu, Mdl, gen, args):
+def bench_stack(torch, dev, gpu, Mdl, gen, args, batches=(1, 16), prefill=True):
     """the quantized linear stack of a 36-layer decoder
     (hidden 2560, 32 q / 8 kv heads of 128, intermediate 9728, vocab 151936),
     every linear GPTQ int4 g128 (lm_head included), random-init packed
@@ -400,7 +416,7 @@ def bench_stack(torch, dev, gpu, Mdl, gen, args):
     out = {"layers": L, "weights_GB": None, "api": "DecoderStack.capture (one HIP graph per token step)"}
     stack = sta.DecoderStack(layers, sta.GptqWeight(lm[0], lm[1], None, None, H, V, GS, TF))
     wbytes = 0
-    for Mb in (1, 16):
+    for Mb in batches:
         b = stack.buffers(gpu, Mb)
         for t in (b.x, b.attn, b.xm):
             t.normal_(generator=gen)
@@ -415,6 +431,11 @@ def bench_stack(torch, dev, gpu, Mdl, gen, args):
                              "hbm_frac": round(tok_bytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
                              "linear_calls_per_step": 4 * L + 1, "qkv": "one concatenated linear"}
         del g, b
+    out["weights_GB"] = round(wbytes / 1e9, 3)
+    if not prefill:
+        del layers, lm, stack
+        torch.cuda.empty_cache()
+        return out
     # Prefill of a 512-token prompt through the same weights with the GEMM
     # (DecoderLinears.prefill: f16 activations and outputs; q|k|v, o, gate,
     # up, and down on silu(gate) * up fused into the GEMM's A pass), then the
