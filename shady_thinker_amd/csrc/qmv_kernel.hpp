@@ -1097,13 +1097,17 @@ int dispatch(st_context *ctx, Params &p, int nsrc, int xm);
 namespace st {
 namespace qmv {
 
-// 1-4 tokens on tiled weights: the streaming kernel (qmv_stream.hpp) from
-// this many 16-column tiles per CU on (graph replay, one token: the int4
-// lm_head 2560 x 151936, 37 tiles per CU, 50.6 -> 42.0 us, and 62.5 -> 43.6
-// us at 4 tokens; at 2-3 tiles per CU it ties (Llama-7B gate/up 12.1 against
-// 12.3 us), and with one tile per CU or fewer the register-ring kernel is
-// 1-2 us faster: q_proj 4.9 against 6.7, down 8.6 against 9.5).
+// 1-4 tokens on tiled weights: the streaming kernel (qmv_stream.hpp) for
+//  * gate/up (two sources) from 2 tiles per CU on, with 8-wave workgroups
+//    (graph replay, one token: Llama-7B 4096 x 2 x 11008 11.7-11.9 -> 10.7-
+//    11.2 us; configs[4] 2560 x 2 x 9728 9.0 -> 7.9-8.3 us);
+//  * one source from this many 16-column tiles per CU on (the int4 lm_head
+//    2560 x 151936, 37 tiles per CU, 50.6 -> 42.0 us, and 62.5 -> 43.6 us at
+//    4 tokens). With one tile per CU or fewer the register-ring kernel is 1-2
+//    us faster on one source (q_proj 4.9 against 6.7, down 8.6 against 9.5),
+//    and at 1.5 tiles per CU too (configs[4] q|k|v 5.7 against 6.3).
 constexpr int kStreamMinTilesCu = 8;
+constexpr int kStreamMinTilesCu2 = 2;  // two sources
 
 // The streaming kernel when it is chosen and the call fits it, else the
 // register-ring kernels.
@@ -1112,7 +1116,9 @@ int launch_fmt(st_context *ctx, Params &p) {
     if constexpr (FMT == FMT_I4T || FMT == FMT_I8T) {
         const int ncu = std::max(1, ctx->num_cus);
         const int pick = tune(ctx, ST_TUNE_DECODE_KERNEL, -1);
-        if (p.M <= 4 && (pick == 1 || (pick < 0 && (p.ntiles + ncu - 1) / ncu >= kStreamMinTilesCu))) {
+        const int tiles_cu = (p.ntiles + ncu - 1) / ncu;
+        const bool auto_stream = NSRC == 2 ? tiles_cu >= kStreamMinTilesCu2 : tiles_cu >= kStreamMinTilesCu;
+        if (p.M <= 4 && (pick == 1 || (pick < 0 && auto_stream))) {
             int rc = -1;
             if constexpr (is_i8(FMT)) {
                 rc = launch_stream<FMT, NSRC, XM, 2, PERM>(ctx, p);

@@ -449,9 +449,11 @@ int launch_stream_nw(st_context *ctx, Params &p, int grid) {
 
 // Launches the streaming kernel when the call fits it; returns -1 (nothing
 // launched) when it does not: the caller then takes the register-ring kernel.
-// Shape: 16 waves per workgroup and one workgroup per CU unless the context
-// settings STREAM_WAVES (8 or 16) / STREAM_TILES_WG (tiles per workgroup)
-// say otherwise.
+// Shape: one workgroup per CU, 16 waves (one source) or 8 (gate/up: 8
+// measured 10.7-11.2 against 11.7 us on Llama-7B's, 7.9-8.3 against 9.8 us
+// on configs[4]'s; 16 and 8 tie on the lm_head), unless the context settings
+// STREAM_WAVES (8 or 16) / STREAM_TILES_WG (tiles per workgroup) say
+// otherwise.
 template <int FMT, int NSRC, int XM, int SPU, bool PERM>
 int launch_stream(st_context *ctx, Params &p) {
     if (p.M > 4 || p.N % kTileN) return -1;
@@ -461,7 +463,8 @@ int launch_stream(st_context *ctx, Params &p) {
     const int ncu = std::max(1, ctx->num_cus);
     const int tpw = tune(ctx, ST_TUNE_STREAM_TILES_WG, 0);
     const int grid = std::min(p.ntiles, tpw > 0 ? (p.ntiles + tpw - 1) / tpw : ncu);
-    if (tune(ctx, ST_TUNE_STREAM_WAVES, 16) == 8) return launch_stream_nw<FMT, NSRC, XM, SPU, PERM, 8>(ctx, p, grid);
+    if (tune(ctx, ST_TUNE_STREAM_WAVES, NSRC == 2 ? 8 : 16) == 8)
+        return launch_stream_nw<FMT, NSRC, XM, SPU, PERM, 8>(ctx, p, grid);
     return launch_stream_nw<FMT, NSRC, XM, SPU, PERM, 16>(ctx, p, grid);
 }
 
