@@ -284,8 +284,10 @@ __global__ __launch_bounds__(64 * NW) void qmv_stream_kernel(Params p) {
         for (int src = 0; src < NSRC; ++src) {
             const unsigned la = lds_addr(wring + (d * NSRC + src) * WB);
             if constexpr (WPU == 2) {
+                // early-clobber outputs: the first read must not land in the
+                // address register the second one still uses
                 asm volatile("ds_read_b32 %0, %2\n\tds_read_b32 %1, %2 offset:256"
-                             : "=v"(w[src][0]), "=v"(w[src][1])
+                             : "=&v"(w[src][0]), "=&v"(w[src][1])
                              : "v"(la + lane * 4u)
                              : "memory");
             } else {

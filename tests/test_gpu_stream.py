@@ -222,3 +222,30 @@ def test_o_proj_cfg4(gpu, orc, Mr):
     e = orc.rel_l2(y, ref)
     print(f"o_proj M={Mr}: rel-L2 {e:.3e}")
     assert e < TOL
+
+
+
+@pytest.mark.parametrize("K,N,gs,Mr,zeros,act,f16", [
+    (2048, 8192, 64, 1, False, False, False),   # two tiles per workgroup, g64 (two 4-byte reads per lane)
+    (1024, 36880, 64, 3, True, True, True),     # 9 tiles per workgroup, zeros, act-order, f16 x
+    (4096, 4096, 128, 1, False, False, False),  # one tile per workgroup
+])
+def test_stream_repeat_launches(gpu, orc, tune, K, N, gs, Mr, zeros, act, f16):
+    """Five launches, bit-identical, against the f64 oracle and the
+    register-ring kernel: a ring read that raced its own address register
+    (two LDS reads in one asm block without early-clobber outputs) once gave
+    a few random wrong tiles per launch on g64."""
+    c = orc.gptq_case(350 + gs + Mr, K, N, gs, zeros=zeros, act_order=act, M=Mr,
+                      x_dtype=np.float16 if f16 else np.float32)
+    w = up(gpu, c)
+    kind = "f16" if f16 else "f32"
+    ref = orc.gptq_matvec_f64(c["x"], c["qweight"], c["scales"], K, N, gs, qzeros=c["qzeros"], g_idx=c["g_idx"])
+    tune(DECODE_KERNEL=STREAM)
+    ys = [run(gpu, kind, w, None, c["x"]) for _ in range(5)]
+    tune(DECODE_KERNEL=RING)
+    y_ring = run(gpu, kind, w, None, c["x"])
+    for y in ys[1:]:
+        assert np.array_equal(y, ys[0])
+    e = orc.rel_l2(ys[0], ref)
+    print(f"stream x5 K={K} N={N} gs={gs} M={Mr}: rel-L2 {e:.3e}")
+    assert e < TOL and orc.rel_l2(ys[0], y_ring) < 1e-6
