@@ -107,6 +107,7 @@ struct Params {
     int grid;      // workgroups
     int nstage;    // COOP: staging waves (they load no weights)
     int ksplit;    // CHK: K slices (1 = none); > 1 writes f32 partials to part
+    int ssync;     // streaming kernel: ring blocks between workgroup barriers (0: none)
     float *part;   // CHK split: [ksplit][NSRC][M][N] partial sums (before the epilogue)
 };
 

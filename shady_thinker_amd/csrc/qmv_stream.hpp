@@ -41,7 +41,10 @@
 namespace st {
 namespace qmv {
 
-constexpr int kStreamRingPerWave = 6 * 1024;  // LDS ring bytes per wave (D is derived from it)
+#ifndef ST_STREAM_RING
+#define ST_STREAM_RING 6144
+#endif
+constexpr int kStreamRingPerWave = ST_STREAM_RING;  // LDS ring bytes per wave (D is derived from it)
 constexpr int kStreamRows = 2;  // x staging: at most two 64-item rows per wave
 constexpr size_t kLdsBytes = 160 * 1024;
 #ifndef ST_STREAM_PRIO
@@ -59,7 +62,9 @@ template <int FMT, int NSRC, int SPU>
 constexpr int stream_depth() {
     constexpr int wb = 256 * stream_wpu<FMT, SPU>();
     constexpr int d = kStreamRingPerWave / (NSRC * wb);
-    return d < 2 ? 2 : (d > 12 ? 12 : d);
+    constexpr int dmax = 63 / (NSRC * (stream_wd<FMT, SPU>() + 2));  // D loads per unit stay below vmcnt's 64
+    constexpr int dc = d > dmax ? dmax : d;
+    return dc < 2 ? 2 : (dc > 12 ? 12 : dc);
 }
 template <int FMT, int NSRC, int SPU, bool HZ>
 constexpr int stream_lpu() {  // loads per unit: weight DMAs + scale (+ zero word); INT8: + its column scale
@@ -90,10 +95,10 @@ __device__ __forceinline__ void dma16(__amdgpu_buffer_rsrc_t r, unsigned char *l
 // Per-wave phase timestamps for probe builds (-DST_STREAM_TRACE); compiled
 // out otherwise.
 #ifdef ST_STREAM_TRACE
-__device__ unsigned long long st_stream_trace[2048 * 16 * 8];
+__device__ unsigned long long st_stream_trace[2048 * 16 * 12];
 #define ST_TR(k) \
     if (lane == 0 && blockIdx.x < 2048) \
-    st_stream_trace[((size_t)blockIdx.x * 16 + wave) * 8 + (k)] = __builtin_amdgcn_s_memrealtime()
+    st_stream_trace[((size_t)blockIdx.x * 16 + wave) * 12 + (k)] = __builtin_amdgcn_s_memrealtime()
 #else
 #define ST_TR(k)
 #endif
@@ -125,7 +130,10 @@ __global__ __launch_bounds__(64 * NW) void qmv_stream_kernel(Params p) {
     const int t0 = (int)((long long)r_wg * p.ntiles / grid);
     const int t1 = (int)((long long)(r_wg + 1) * p.ntiles / grid);
     const int U = (t1 - t0) * G;  // units of the workgroup (per source)
-    const int ua = (int)((long long)wave * U / NW), ub = (int)((long long)(wave + 1) * U / NW);
+    // wave w's units [range(w), range(w + 1)) (32-bit: the host keeps U * NW
+    // below 2^31; NW is a power of two, so this is a multiply and a shift)
+    const auto range = [&](int w) { return (int)((unsigned)w * (unsigned)U / (unsigned)NW); };
+    const int ua = range(wave), ub = range(wave + 1);
     const int nu = ub - ua;
     ST_TR(0);
 
@@ -204,7 +212,11 @@ __global__ __launch_bounds__(64 * NW) void qmv_stream_kernel(Params p) {
             if constexpr (is_i8(FMT)) {
                 meta[src][d] = __builtin_amdgcn_raw_buffer_load_b32(rs0, vlane_s, soff, 0);
             } else {
+#ifdef ST_PROBE_NOSCALE
+                meta[src][d] = __builtin_amdgcn_raw_buffer_load_b16(src == 0 ? rs0 : rs1, 0u, 0u, 0);
+#else
                 meta[src][d] = __builtin_amdgcn_raw_buffer_load_b16(src == 0 ? rs0 : rs1, vlane_s, soff, 0);
+#endif
                 if constexpr (HZ) zw[src][d] = __builtin_amdgcn_raw_buffer_load_b32(src == 0 ? rz0 : rz1, vlane_z, zoff, 0);
             }
         }
@@ -312,6 +324,14 @@ __global__ __launch_bounds__(64 * NW) void qmv_stream_kernel(Params p) {
 #pragma unroll
         for (int st = 0; st < SPU; ++st) asm volatile("" : "+v"(A[st]));
         asm volatile("" : "+v"(es));
+#ifdef ST_PROBE_NOCOMPUTE
+#pragma unroll
+        for (int src = 0; src < NSRC; ++src)
+            tot[src] += __builtin_bit_cast(float, (w[src][0] ^ A[0].x ^ es.x ^ meta[src][d]) & 0x3FFFFFu);
+        if (false) {
+#else
+        {
+#endif
         v4i acc[NSRC];
 #pragma unroll
         for (int src = 0; src < NSRC; ++src) {
@@ -346,6 +366,7 @@ __global__ __launch_bounds__(64 * NW) void qmv_stream_kernel(Params p) {
             const int lo = (S.y << 8) + S.z + __mul24(z, nl);
             tot[src] = fmaf(fmaf((float)hi, 65536.0f, (float)lo), f, tot[src]);
         }
+        }
         // end of a tile, or of this wave's range (a scalar test): full tiles
         // go out, partial ones to LDS (slot 0: the tile began before this
         // range; slot 1: it began in it and runs on past it)
@@ -377,14 +398,27 @@ __global__ __launch_bounds__(64 * NW) void qmv_stream_kernel(Params p) {
     // finish first and the youngest run the last part alone with a quarter
     // of the loads in flight. A wave lowers its priority as its remaining
     // share shrinks (quarters of its range), which keeps the waves level.
+    //
+    // Every ssync ring blocks the workgroup meets at a bare s_barrier (the
+    // DMAs stay in flight): the waves ahead wait there with full rings, so
+    // the memory queue serves the waves behind. Every wave runs the same
+    // number of blocks (the largest range's), so every wave meets every
+    // barrier; blocks past a wave's own range compute nothing.
     int prio = 3;
+    const int numax = (U + NW - 1) / NW;  // no wave's range is longer
+    const int ssync = p.ssync;
+    int scount = 0;
     __builtin_amdgcn_s_setprio(3);
-    for (int i0 = 0; i0 < nu; i0 += D) {
+    for (int i0 = 0; i0 < numax; i0 += D) {
 #pragma unroll
         for (int d = 0; d < D; ++d) {
             if (i0 + d < nu) compute(i0 + d, d);
             if (i0 + d == 0) ST_TR(7);
             issue(i0 + d + D, d);  // always: the count of loads per unit is fixed
+        }
+        if (ssync > 0 && ++scount == ssync) {
+            scount = 0;
+            asm volatile("s_barrier" ::: "memory");
         }
         const int rem = nu - (i0 + D);  // units left after this block
         const int tp = rem <= 0 ? 0 : min(3, rem * 4 / nu);
@@ -403,23 +437,43 @@ __global__ __launch_bounds__(64 * NW) void qmv_stream_kernel(Params p) {
     if (nu > 0) {
         const int tl = (ub - 1) / G, ts = tl * G, te = ts + G;
         if (ts >= ua && te > ub) {  // began in this range, continues past it: this wave finishes it
-            // the later waves' first-tile partials, read all at once (no
-            // dependent chain), added in wave order
-            float v[NSRC];
-#pragma unroll
-            for (int src = 0; src < NSRC; ++src) v[src] = red[((wave * 2 + 1) * NSRC + src) * 64 + lane];
+            ST_TR(10);
+            // the first-tile partials of the later waves whose ranges begin
+            // inside this tile, added in wave order, without branches (after
+            // the barrier the four waves of a SIMD run this part one after
+            // another, oldest first, and a taken scalar branch costs tens of
+            // cycles): range(w) < te <=> w U < te NW, so the last such wave
+            // is (te NW - 1) / U; the reads are all issued before the adds,
+            // and a partial left out is masked to +0 (its slot may hold
+            // anything, so no multiply by 0)
+            const int wl = min(NW - 1, (int)(((unsigned)te * NW - 1u) / (unsigned)U));
+            float r[NW - 1][NSRC];
 #pragma unroll
             for (int k = 1; k < NW; ++k) {
                 const int w2 = min(wave + k, NW - 1);
-                const int a2 = (int)((long long)w2 * U / NW), b2 = (int)((long long)(w2 + 1) * U / NW);
-                const bool inc = wave + k < NW && a2 < te && a2 < b2;
 #pragma unroll
-                for (int src = 0; src < NSRC; ++src) {
-                    const float r = red[((w2 * 2) * NSRC + src) * 64 + lane];
-                    v[src] += inc ? r : 0.0f;
-                }
+                for (int src = 0; src < NSRC; ++src) r[k - 1][src] = red[((w2 * 2) * NSRC + src) * 64 + lane];
             }
+            float v[NSRC];
+#pragma unroll
+            for (int src = 0; src < NSRC; ++src) v[src] = red[((wave * 2 + 1) * NSRC + src) * 64 + lane];
+            // U >= NW: no range is empty; else a wave with an empty range wrote no partial
+            const unsigned nonempty = U >= NW ? 0xFFFFu : [&] {
+                unsigned m = 0;
+                for (int w2 = 0; w2 < NW; ++w2) m |= (range(w2) < range(w2 + 1) ? 1u : 0u) << w2;
+                return m;
+            }();
+#pragma unroll
+            for (int k = 1; k < NW; ++k) {
+                const int w2 = wave + k;
+                const unsigned keep = (w2 <= wl && ((nonempty >> (w2 & 15)) & 1u)) ? ~0u : 0u;
+#pragma unroll
+                for (int src = 0; src < NSRC; ++src)
+                    v[src] += __builtin_bit_cast(float, __builtin_bit_cast(unsigned, r[k - 1][src]) & keep);
+            }
+            ST_TR(8);
             write_y(t0 + tl, v, is_i8(FMT) ? p.scale8[(t0 + tl) * kTileN + c] : 0.0f);
+            ST_TR(9);
         }
     }
     ST_TR(6);
@@ -462,9 +516,12 @@ int launch_stream(st_context *ctx, Params &p) {
     // 32-bit buffer offsets (weights, scales, zero words)
     if ((size_t)p.ntiles * kTileN * p.K / 2 * (is_i8(FMT) ? 2 : 1) >= (size_t(1) << 31)) return -1;
     p.rb = 4 * p.M;
+    p.ssync = std::max(0, tune(ctx, ST_TUNE_STREAM_SYNC, 0));
     const int ncu = std::max(1, ctx->num_cus);
     const int tpw = tune(ctx, ST_TUNE_STREAM_TILES_WG, 0);
     const int grid = std::min(p.ntiles, tpw > 0 ? (p.ntiles + tpw - 1) / tpw : ncu);
+    // the kernel splits a workgroup's units over its waves in 32-bit arithmetic
+    if ((long long)((p.ntiles + grid - 1) / grid) * p.units * 16 >= (1LL << 31)) return -1;
     if (tune(ctx, ST_TUNE_STREAM_WAVES, NSRC == 2 ? 8 : 16) == 8)
         return launch_stream_nw<FMT, NSRC, XM, SPU, PERM, 8>(ctx, p, grid);
     return launch_stream_nw<FMT, NSRC, XM, SPU, PERM, 16>(ctx, p, grid);

@@ -94,6 +94,8 @@ def test_stream_matches_oracle_and_ring(gpu, orc, tune, K, N, gs, Mr, zeros, zp1
     tune(DECODE_KERNEL=STREAM)
     y = run(gpu, kind, w, w2, x, b)
     y_again = run(gpu, kind, w, w2, x, b)
+    tune(DECODE_KERNEL=STREAM, STREAM_SYNC=1)  # a workgroup barrier after every ring block: same sums
+    y_sync = run(gpu, kind, w, w2, x, b)
     tune(DECODE_KERNEL=RING)
     y_ring = run(gpu, kind, w, w2, x, b)
 
@@ -110,6 +112,7 @@ def test_stream_matches_oracle_and_ring(gpu, orc, tune, K, N, gs, Mr, zeros, zp1
     print(f"stream K={K} N={N} gs={gs} M={Mr} {kind}: rel-L2 {e:.3e} vs ring {orc.rel_l2(y, y_ring):.2e}")
     assert np.isfinite(y).all() and e < TOL
     assert np.array_equal(y, y_again)  # deterministic
+    assert np.array_equal(y, y_sync)
     assert orc.rel_l2(y, y_ring) < 1e-6
 
 
