@@ -830,8 +830,20 @@ __global__ __launch_bounds__((64 * (CM == 3 ? kChunkWaves<NSRC, MB> : kMaxWavesF
         float v[NSRC];
 #pragma unroll
         for (int src = 0; src < NSRC; ++src) {
+            // the WPT slices of the tile, in slice order: every read issued
+            // before the first add (a loop of dependent LDS reads costs ~0.05
+            // us a slice), slots past the last slice masked to +0
+            constexpr int SMAX = CM == 3 ? kChunkWaves<NSRC, MB> : kMaxWavesFor<NSRC, (CM != 0)>;
+            float r[SMAX];
+#pragma unroll
+            for (int k = 0; k < SMAX; ++k) {
+                const int w = min(wave + k * TB, TB * WPT - 1);
+                r[k] = red[(((NS + w) * NSRC + src) * MB + mb) * 64 + lane];
+            }
             float a = 0.0f;
-            for (int w = wave; w < TB * WPT; w += TB) a += red[(((NS + w) * NSRC + src) * MB + mb) * 64 + lane];
+#pragma unroll
+            for (int k = 0; k < SMAX; ++k)
+                a += __builtin_bit_cast(float, __builtin_bit_cast(unsigned, r[k]) & (k < WPT ? ~0u : 0u));
             v[src] = a;
         }
         if (m >= M || n >= N) continue;
