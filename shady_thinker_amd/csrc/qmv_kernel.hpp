@@ -305,6 +305,17 @@ __device__ __forceinline__ void quantize_item(float (&v)[16], bool ok, u32x4 *ds
     }
 }
 
+// Per-wave phase timestamps for probe builds (-DST_STREAM_TRACE), used by
+// both decode kernels; compiled out otherwise.
+#ifdef ST_STREAM_TRACE
+__device__ unsigned long long st_stream_trace[2048 * 16 * 12];
+#define ST_TR(k) \
+    if (lane == 0 && blockIdx.x < 2048) \
+    st_stream_trace[((size_t)blockIdx.x * 16 + wave) * 12 + (k)] = __builtin_amdgcn_s_memrealtime()
+#else
+#define ST_TR(k)
+#endif
+
 // s_waitcnt vmcnt(0) (expcnt and lgkmcnt left at their maxima).
 __device__ __forceinline__ void wait_vm_all() { __builtin_amdgcn_s_waitcnt(0x0F70); }
 
@@ -724,12 +735,21 @@ __global__ __launch_bounds__((64 * (CM == 3 ? kChunkWaves<NSRC, MB> : kMaxWavesF
     // once. Nothing is in flight across the branch. Fallback: x first (loads complete in issue order),
     // then the ring, then the staging.
     const int cs0 = (COOP && !PW) ? 0 : u0;
+    ST_TR(0);
     if (COOP && !PW && wave < NS) {
         xload(cs0);
         wait_vm_all();
+        ST_TR(1);
         stage(cs0);
     }
+    ST_TR(2);
     if (PW) xload(cs0);  // (a wave without groups has no items: uniform skip inside)
+    // per-wave staging: every wave's x loads enter the CU's memory queue
+    // before any weight load (the waves of a workgroup start up to ~0.6 us
+    // apart, and a late wave's x would otherwise wait behind the early
+    // waves' weights: configs[4] down 7.2 -> 6.8 us); a bare barrier (no
+    // wait for loads), met by every wave
+    if constexpr (PW) asm volatile("s_barrier" ::: "memory");
     if (!COOP && u0 < u1) xload(cs0);
     // COOP GPTQ: the scales of the wave's (at most kScaleUnits) groups for
     // the tile's 16 columns in two 4-byte loads per lane and source (lane l,
@@ -772,6 +792,7 @@ __global__ __launch_bounds__((64 * (CM == 3 ? kChunkWaves<NSRC, MB> : kMaxWavesF
         // flight (vmcnt(0)), i.e. for the ring. The asm's memory clobber
         // keeps the compiler from moving LDS accesses across it.
         asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+        ST_TR(3);
         // the rest of the ring, after the barrier: issuing it can stall while
         // the CU's memory queue is full, and that must not hold up the barrier
 #pragma unroll
@@ -794,6 +815,7 @@ __global__ __launch_bounds__((64 * (CM == 3 ? kChunkWaves<NSRC, MB> : kMaxWavesF
                     ui = 0;
                     next_chunk(u);
                 }
+                if (u == u0) ST_TR(7);
                 compute(ring[d], u, ui);
                 ++ui;
                 load_unit(ring[d], min(u + D, u1 - 1), u + D < u1);
@@ -816,13 +838,18 @@ __global__ __launch_bounds__((64 * (CM == 3 ? kChunkWaves<NSRC, MB> : kMaxWavesF
     }
 
     // ------------------------------------------- reduce the waves, write y
+    ST_TR(4);
     float *red = reinterpret_cast<float *>(smem + (COOP ? (size_t)p.wave_lds : (size_t)NW * p.wave_lds));
 #pragma unroll
     for (int src = 0; src < NSRC; ++src)
 #pragma unroll
         for (int mb = 0; mb < MB; ++mb) red[((wave * NSRC + src) * MB + mb) * 64 + lane] = tot[src][mb];
     __syncthreads();
-    if (wave >= TB) return;  // wave j (< TB) sums the K slices of tile t0 + j, in slice order
+    ST_TR(5);
+    if (wave >= TB) {
+        ST_TR(6);
+        return;
+    }  // wave j (< TB) sums the K slices of tile t0 + j, in slice order
     const int n = (t0 + wave) * kTileN + c;  // column of tile t0 + wave
 #pragma unroll
     for (int mb = 0; mb < MB; ++mb) {
@@ -857,6 +884,7 @@ __global__ __launch_bounds__((64 * (CM == 3 ? kChunkWaves<NSRC, MB> : kMaxWavesF
         if constexpr (is_i8(FMT)) out *= p.scale8[n];
         p.y[(size_t)m * N + n] = out;
     }
+    ST_TR(6);
 }
 
 // CHK split-K: y[m, n] = epilogue(sum over s < S of part[s][src][m][n]), the

@@ -92,16 +92,6 @@ __device__ __forceinline__ void dma16(__amdgpu_buffer_rsrc_t r, unsigned char *l
     __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (__attribute__((address_space(3))) void *)lds, 16, off, 0, 0, AUX);
 }
 
-// Per-wave phase timestamps for probe builds (-DST_STREAM_TRACE); compiled
-// out otherwise.
-#ifdef ST_STREAM_TRACE
-__device__ unsigned long long st_stream_trace[2048 * 16 * 12];
-#define ST_TR(k) \
-    if (lane == 0 && blockIdx.x < 2048) \
-    st_stream_trace[((size_t)blockIdx.x * 16 + wave) * 12 + (k)] = __builtin_amdgcn_s_memrealtime()
-#else
-#define ST_TR(k)
-#endif
 
 template <int FMT, int NSRC, int XM, int SPU, bool PERM, bool HZ, int NW>
 __global__ __launch_bounds__(64 * NW) void qmv_stream_kernel(Params p) {
