@@ -1140,13 +1140,14 @@ namespace qmv {
 
 // 1-4 tokens on tiled weights: the streaming kernel (qmv_stream.hpp) for
 //  * gate/up (two sources) from 2 tiles per CU on, with 8-wave workgroups
-//    (graph replay, one token: Llama-7B 4096 x 2 x 11008 11.7-11.9 -> 10.7-
-//    11.2 us; configs[4] 2560 x 2 x 9728 9.0 -> 7.9-8.3 us);
+//    (graph replay, one token: Llama-7B 4096 x 2 x 11008 12.2 -> 10.4-11.1
+//    us; configs[4] 2560 x 2 x 9728 9.1-9.3 -> 7.7-8.2 us);
 //  * one source from this many 16-column tiles per CU on (the int4 lm_head
-//    2560 x 151936, 37 tiles per CU, 50.6 -> 42.0 us, and 62.5 -> 43.6 us at
-//    4 tokens). With one tile per CU or fewer the register-ring kernel is 1-2
-//    us faster on one source (q_proj 4.9 against 6.7, down 8.6 against 9.5),
-//    and at 1.5 tiles per CU too (configs[4] q|k|v 5.7 against 6.3).
+//    2560 x 151936, 37 tiles per CU, 51 -> 39-42 us, and 62.5 -> 43 us at
+//    4 tokens). With one tile per CU or fewer the register-ring kernel is
+//    0.4-1 us faster on one source (q_proj 4.7 against 5.7, down 7.9 against
+//    8.8, configs[4] o 4.4 against 5.6), and at 1.5 tiles per CU too
+//    (configs[4] q|k|v 5.8 against 6.1).
 constexpr int kStreamMinTilesCu = 8;
 constexpr int kStreamMinTilesCu2 = 2;  // two sources
 
