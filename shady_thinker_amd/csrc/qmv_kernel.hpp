@@ -1141,15 +1141,19 @@ namespace qmv {
 // 1-4 tokens on tiled weights: the streaming kernel (qmv_stream.hpp) for
 //  * gate/up (two sources) from 2 tiles per CU on, with 8-wave workgroups
 //    (graph replay, one token: Llama-7B 4096 x 2 x 11008 12.2 -> 10.4-11.1
-//    us; configs[4] 2560 x 2 x 9728 9.1-9.3 -> 7.7-8.2 us);
-//  * one source from this many 16-column tiles per CU on (the int4 lm_head
-//    2560 x 151936, 37 tiles per CU, 51 -> 39-42 us, and 62.5 -> 43 us at
-//    4 tokens). With one tile per CU or fewer the register-ring kernel is
-//    0.4-1 us faster on one source (q_proj 4.7 against 5.7, down 7.9 against
-//    8.8, configs[4] o 4.4 against 5.6), and at 1.5 tiles per CU too
-//    (configs[4] q|k|v 5.8 against 6.1).
+//    us; configs[4] 2560 x 2 x 9728 9.1-9.3 -> 7.7-8.2 us; at 4 tokens 16.8
+//    -> 13.0 us);
+//  * one source from kStreamMinTilesCu tiles per CU on, with 16-wave
+//    workgroups (the int4 lm_head 2560 x 151936, 37 tiles per CU: 51 ->
+//    39-42 us, 65 -> 43 us at 4 tokens; 8 waves are 1.5-2 us slower);
+//  * one source with 2-4 tokens from 2 tiles per CU on, with 8-wave
+//    workgroups (4096 x 11008: 9.0 / 11.5 / 14.6-15.1 -> 8.7 / 8.8 / 10.0 us
+//    at 2 / 3 / 4 tokens; one token is a tie, 7.9-8.5 us either way).
+// With fewer tiles the register-ring kernel is 0.2-1 us faster (q_proj
+// 4.7 against 5.6, down 7.9 against 8.8, configs[4] o 4.4 against 5.6 and
+// q|k|v, 1.5 tiles per CU, 5.9-6.3 against 6.0-6.5).
 constexpr int kStreamMinTilesCu = 8;
-constexpr int kStreamMinTilesCu2 = 2;  // two sources
+constexpr int kStreamMinTilesCu2 = 2;  // two sources; one source with 2+ tokens
 
 // The streaming kernel when it is chosen and the call fits it, else the
 // register-ring kernels.
@@ -1159,16 +1163,19 @@ int launch_fmt(st_context *ctx, Params &p) {
         const int ncu = std::max(1, ctx->num_cus);
         const int pick = tune(ctx, ST_TUNE_DECODE_KERNEL, -1);
         const int tiles_cu = (p.ntiles + ncu - 1) / ncu;
-        const bool auto_stream = NSRC == 2 ? tiles_cu >= kStreamMinTilesCu2 : tiles_cu >= kStreamMinTilesCu;
+        const bool many = NSRC == 1 && tiles_cu >= kStreamMinTilesCu;  // 16-wave workgroups
+        const bool auto_stream = NSRC == 2 ? tiles_cu >= kStreamMinTilesCu2
+                                           : (many || (p.M >= 2 && p.ntiles >= kStreamMinTilesCu2 * ncu));
+        const int waves = many ? 16 : 8;
         if (p.M <= 4 && (pick == 1 || (pick < 0 && auto_stream))) {
             int rc = -1;
             if constexpr (is_i8(FMT)) {
-                rc = launch_stream<FMT, NSRC, XM, 2, PERM>(ctx, p);
+                rc = launch_stream<FMT, NSRC, XM, 2, PERM>(ctx, p, waves);
             } else {
                 switch (p.gs) {
-                    case 64: rc = launch_stream<FMT, NSRC, XM, 1, PERM>(ctx, p); break;
-                    case 128: rc = launch_stream<FMT, NSRC, XM, 2, PERM>(ctx, p); break;
-                    case 256: rc = launch_stream<FMT, NSRC, XM, 4, PERM>(ctx, p); break;
+                    case 64: rc = launch_stream<FMT, NSRC, XM, 1, PERM>(ctx, p, waves); break;
+                    case 128: rc = launch_stream<FMT, NSRC, XM, 2, PERM>(ctx, p, waves); break;
+                    case 256: rc = launch_stream<FMT, NSRC, XM, 4, PERM>(ctx, p, waves); break;
                 }
             }
             if (rc != -1) return rc;

@@ -45,7 +45,10 @@ namespace qmv {
 #define ST_STREAM_RING 6144
 #endif
 constexpr int kStreamRingPerWave = ST_STREAM_RING;  // LDS ring bytes per wave (D is derived from it)
-constexpr int kStreamRows = 2;  // x staging: at most two 64-item rows per wave
+// x staging: at most this many 64-item rows per wave (8-wave workgroups have
+// the registers for three: up to 256 VGPRs a wave)
+template <int NW>
+constexpr int kStreamRows = NW == 8 ? 3 : 2;
 constexpr size_t kLdsBytes = 160 * 1024;
 #ifndef ST_STREAM_PRIO
 #define ST_STREAM_PRIO 1
@@ -102,7 +105,7 @@ __global__ __launch_bounds__(64 * NW) void qmv_stream_kernel(Params p) {
     constexpr int D = stream_depth<FMT, NSRC, SPU>();
     constexpr int LPU = stream_lpu<FMT, NSRC, SPU, HZ>();
     static_assert(D * LPU < 64, "ring wait exceeds vmcnt");
-    constexpr int RMAX = kStreamRows;
+    constexpr int RMAX = kStreamRows<NW>;
     __shared__ __align__(16) unsigned char ring[stream_ring_bytes<FMT, NSRC, SPU, NW>()];
     extern __shared__ __align__(16) unsigned char smem[];  // A operands, es, a zero block, partial sums
 
@@ -474,7 +477,7 @@ __global__ __launch_bounds__(64 * NW) void qmv_stream_kernel(Params p) {
 template <int FMT, int NSRC, int XM, int SPU, bool PERM, int NW>
 int launch_stream_nw(st_context *ctx, Params &p, int grid) {
     const int items = p.M * p.units * 4 * SPU;
-    if (items > 64 * kStreamRows * NW) return -1;
+    if (items > 64 * kStreamRows<NW> * NW) return -1;
     const size_t dyn = (size_t)p.units * SPU * 4 * p.rb * 16 + (size_t)p.units * p.M * 16 + (size_t)SPU * 4 * p.rb * 16 +
                        (size_t)NW * 2 * NSRC * 64 * sizeof(float);
     if (dyn + stream_ring_bytes<FMT, NSRC, SPU, NW>() > kLdsBytes) return -1;
@@ -495,13 +498,11 @@ int launch_stream_nw(st_context *ctx, Params &p, int grid) {
 
 // Launches the streaming kernel when the call fits it; returns -1 (nothing
 // launched) when it does not: the caller then takes the register-ring kernel.
-// Shape: one workgroup per CU, 16 waves (one source) or 8 (gate/up: 8
-// measured 10.7-11.2 against 11.7 us on Llama-7B's, 7.9-8.3 against 9.8 us
-// on configs[4]'s; 16 and 8 tie on the lm_head), unless the context settings
-// STREAM_WAVES (8 or 16) / STREAM_TILES_WG (tiles per workgroup) say
-// otherwise.
+// Shape: one workgroup per CU of `waves` waves (the caller's choice, 8 or
+// 16), unless the context settings STREAM_WAVES (8 or 16) / STREAM_TILES_WG
+// (tiles per workgroup) say otherwise.
 template <int FMT, int NSRC, int XM, int SPU, bool PERM>
-int launch_stream(st_context *ctx, Params &p) {
+int launch_stream(st_context *ctx, Params &p, int waves) {
     if (p.M > 4 || p.N % kTileN) return -1;
     // 32-bit buffer offsets (weights, scales, zero words)
     if ((size_t)p.ntiles * kTileN * p.K / 2 * (is_i8(FMT) ? 2 : 1) >= (size_t(1) << 31)) return -1;
@@ -512,7 +513,7 @@ int launch_stream(st_context *ctx, Params &p) {
     const int grid = std::min(p.ntiles, tpw > 0 ? (p.ntiles + tpw - 1) / tpw : ncu);
     // the kernel splits a workgroup's units over its waves in 32-bit arithmetic
     if ((long long)((p.ntiles + grid - 1) / grid) * p.units * 16 >= (1LL << 31)) return -1;
-    if (tune(ctx, ST_TUNE_STREAM_WAVES, NSRC == 2 ? 8 : 16) == 8)
+    if (tune(ctx, ST_TUNE_STREAM_WAVES, waves) == 8)
         return launch_stream_nw<FMT, NSRC, XM, SPU, PERM, 8>(ctx, p, grid);
     return launch_stream_nw<FMT, NSRC, XM, SPU, PERM, 16>(ctx, p, grid);
 }

@@ -96,6 +96,10 @@ def test_stream_matches_oracle_and_ring(gpu, orc, tune, K, N, gs, Mr, zeros, zp1
     y_again = run(gpu, kind, w, w2, x, b)
     tune(DECODE_KERNEL=STREAM, STREAM_SYNC=1)  # a workgroup barrier after every ring block: same sums
     y_sync = run(gpu, kind, w, w2, x, b)
+    ys_nw = {}
+    for nw in (8, 16):  # both workgroup shapes, whichever the routing picks
+        tune(DECODE_KERNEL=STREAM, STREAM_SYNC=0, STREAM_WAVES=nw)
+        ys_nw[nw] = run(gpu, kind, w, w2, x, b)
     tune(DECODE_KERNEL=RING)
     y_ring = run(gpu, kind, w, w2, x, b)
 
@@ -113,6 +117,8 @@ def test_stream_matches_oracle_and_ring(gpu, orc, tune, K, N, gs, Mr, zeros, zp1
     assert np.isfinite(y).all() and e < TOL
     assert np.array_equal(y, y_again)  # deterministic
     assert np.array_equal(y, y_sync)
+    for nw, yn in ys_nw.items():
+        assert orc.rel_l2(yn, ref) < TOL and orc.rel_l2(yn, y_ring) < 1e-6, nw
     assert orc.rel_l2(y, y_ring) < 1e-6
 
 
@@ -252,3 +258,26 @@ def test_stream_repeat_launches(gpu, orc, tune, K, N, gs, Mr, zeros, act, f16):
     e = orc.rel_l2(ys[0], ref)
     print(f"stream x5 K={K} N={N} gs={gs} M={Mr}: rel-L2 {e:.3e}")
     assert e < TOL and orc.rel_l2(ys[0], y_ring) < 1e-6
+
+
+@pytest.mark.parametrize("Mr", [2, 3, 4])
+def test_multi_token_routing(gpu, orc, Mr):
+    """2-4 tokens on one source with 2+ tiles per CU go to the streaming
+    kernel with 8-wave workgroups (three staging rows per wave): GPTQ 4096 x
+    11008 (688 tiles) with f32 x, and INT8 configs[2] 5120 x 13824 with f32 x
+    (at 4 tokens its 1280 staging items need the third row). Default
+    routing, every row against the f64 oracle."""
+    c = orc.gptq_case(360 + Mr, 4096, 11008, 128, zeros=True, M=Mr)
+    w = up(gpu, c)
+    y = run(gpu, "f32", w, None, c["x"])
+    ref = orc.gptq_matvec_f64(c["x"], c["qweight"], c["scales"], 4096, 11008, 128, qzeros=c["qzeros"])
+    e = orc.rel_l2(y, ref)
+    K8, N8 = 5120, 13824
+    c8 = orc.int8_case(370 + Mr, K8, N8, M=Mr, x_dtype=np.float32)
+    w8 = sta.Int8Weight.upload(gpu, c8["w"], c8["scale"])
+    y8 = torch.empty(Mr, N8, device="cuda")
+    M.int8_matvec(gpu, dev(c8["x"]), w8.w, w8.scale, y8, K8, N8, w8.flags)
+    torch.cuda.synchronize()
+    e8 = orc.rel_l2(y8.cpu().numpy(), orc.int8_matvec_f64(c8["x"], c8["w"], c8["scale"], K8, N8))
+    print(f"multi-token routing M={Mr}: GPTQ rel-L2 {e:.3e}, INT8 {e8:.3e}")
+    assert e < TOL and e8 < TOL
