@@ -113,6 +113,7 @@ typedef enum {
     ST_TUNE_STREAM_WAVES,      /* streaming decode kernel: waves per workgroup (8 or 16) */
     ST_TUNE_STREAM_TILES_WG,   /* streaming decode kernel: 16-column tiles per workgroup (0: a workgroup per CU) */
     ST_TUNE_STREAM_SYNC,       /* streaming decode kernel: ring blocks between workgroup barriers (0: none) */
+    ST_TUNE_SPLIT_REDUCE_KERNEL, /* several-token split-K decode: 1 reduce kernel, 0 fused (default: fused up to 8 tokens) */
     ST_TUNE_COUNT
 } st_tune;
 int st_context_set_tune(st_context *ctx, int knob, int value);

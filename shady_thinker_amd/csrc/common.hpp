@@ -21,6 +21,9 @@ struct st_context {
     // what it uses; calls on one context are ordered by its stream).
     float *ws = nullptr;
     size_t ws_bytes = 0;
+    // split-K counters of the decode kernels (kSplitCounters words, zero
+    // between calls: the last slice of each tile group clears its own)
+    unsigned *split_counters = nullptr;
     // the no-allocation entry point's scratch on this context's GPU (the
     // device address of runtime.hip's static array)
     void *scratch = nullptr;
@@ -32,6 +35,8 @@ struct st_context {
 };
 
 namespace st {
+
+constexpr int kSplitCounters = 4096;
 
 // A kernel-path setting of the context, or `dflt` when it is automatic.
 inline int tune(const st_context *ctx, int knob, int dflt) {

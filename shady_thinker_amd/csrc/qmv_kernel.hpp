@@ -109,6 +109,7 @@ struct Params {
     int ksplit;    // CHK: K slices (1 = none); > 1 writes f32 partials to part
     int ssync;     // streaming kernel: ring blocks between workgroup barriers (0: none)
     float *part;   // CHK split: [ksplit][NSRC][M][N] partial sums (before the epilogue)
+    unsigned *cnt; // CHK split: per tile group, slices done (zero between calls); NULL: a reduce kernel follows
 };
 
 // silu(v) = v / (1 + exp(-v)) (fused_silu_gptq.wgsl:19-21), with the hardware
@@ -304,6 +305,8 @@ __device__ __forceinline__ void quantize_item(float (&v)[16], bool ok, u32x4 *ds
         *es_dst = u32x4{__builtin_bit_cast(unsigned, em), (unsigned)(-h), (unsigned)(-(sum - (h << 16))), 0u};
     }
 }
+
+constexpr int kMaxKSplit = 16;  // CHK split-K: most K slices
 
 // Per-wave phase timestamps for probe builds (-DST_STREAM_TRACE), used by
 // both decode kernels; compiled out otherwise.
@@ -846,13 +849,21 @@ __global__ __launch_bounds__((64 * (CM == 3 ? kChunkWaves<NSRC, MB> : kMaxWavesF
         for (int mb = 0; mb < MB; ++mb) red[((wave * NSRC + src) * MB + mb) * 64 + lane] = tot[src][mb];
     __syncthreads();
     ST_TR(5);
-    if (wave >= TB) {
+    // split K with the reduction fused (p.cnt): every slice writes its
+    // partial through to memory (sc0 sc1 stores, completed before the
+    // counter), the last of the tile group's slices to count in adds them in
+    // slice order and writes y. Nobody waits for anybody.
+    const bool fused = CHK && KS > 1 && p.cnt != nullptr;
+    if (!fused && wave >= TB) {
         ST_TR(6);
         return;
     }  // wave j (< TB) sums the K slices of tile t0 + j, in slice order
     const int n = (t0 + wave) * kTileN + c;  // column of tile t0 + wave
+    const __amdgpu_buffer_rsrc_t rpart =
+        __builtin_amdgcn_make_buffer_rsrc((void *)p.part, (short)0, 0x7FFFFFFF, kBufWord3);
+    constexpr int kCoherent = 1 | 16;  // sc0 sc1: write through / read past this XCD's L2
 #pragma unroll
-    for (int mb = 0; mb < MB; ++mb) {
+    for (int mb = 0; mb < MB && wave < TB; ++mb) {
         const int m = mb * 4 + q;
         float v[NSRC];
 #pragma unroll
@@ -874,15 +885,60 @@ __global__ __launch_bounds__((64 * (CM == 3 ? kChunkWaves<NSRC, MB> : kMaxWavesF
             v[src] = a;
         }
         if (m >= M || n >= N) continue;
-        if (KS > 1) {  // split-K partial: the reduce kernel applies the epilogue
+        if (KS > 1) {  // split-K partial: the reduce (fused below, or a kernel) applies the epilogue
 #pragma unroll
-            for (int src = 0; src < NSRC; ++src) p.part[(((size_t)ksp * NSRC + src) * M + m) * N + n] = v[src];
+            for (int src = 0; src < NSRC; ++src) {
+                const unsigned off = (unsigned)(((((size_t)ksp * NSRC + src) * M + m) * N + n) * 4);
+                if (fused)
+                    __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(unsigned, v[src]), rpart, off, 0, kCoherent);
+                else
+                    p.part[(((size_t)ksp * NSRC + src) * M + m) * N + n] = v[src];
+            }
             continue;
         }
         float out = v[0];
         if constexpr (NSRC == 2) out = silu_f(v[0]) * v[1];
         if constexpr (is_i8(FMT)) out *= p.scale8[n];
         p.y[(size_t)m * N + n] = out;
+    }
+    if (fused) {
+        __shared__ unsigned s_last;
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // this wave's partials are in memory
+        __syncthreads();
+        if (tid == 0) {
+            const unsigned done = __hip_atomic_fetch_add(&p.cnt[b], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+            s_last = done == (unsigned)KS - 1;
+            if (s_last)  // every slice has counted in: clear for the next call
+                __hip_atomic_store(&p.cnt[b], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+        }
+        __syncthreads();
+        if (s_last && wave < TB) {
+#pragma unroll
+            for (int mb = 0; mb < MB; ++mb) {
+                const int m = mb * 4 + q;
+                if (m >= M || n >= N) continue;
+                float v[NSRC];
+#pragma unroll
+                for (int src = 0; src < NSRC; ++src) {
+                    // every slice's load in flight at once (slots past KS read
+                    // nothing: an offset past the buffer), then the adds in order
+                    unsigned r[kMaxKSplit];
+#pragma unroll
+                    for (int k = 0; k < kMaxKSplit; ++k)
+                        r[k] = __builtin_amdgcn_raw_buffer_load_b32(
+                            rpart, k < KS ? (unsigned)(((((size_t)k * NSRC + src) * M + m) * N + n) * 4) : kNoLoad, 0,
+                            kCoherent);
+                    float a = 0.0f;
+#pragma unroll
+                    for (int k = 0; k < kMaxKSplit; ++k) a += __builtin_bit_cast(float, r[k] & (k < KS ? ~0u : 0u));
+                    v[src] = a;
+                }
+                float out = v[0];
+                if constexpr (NSRC == 2) out = silu_f(v[0]) * v[1];
+                if constexpr (is_i8(FMT)) out *= p.scale8[n];
+                p.y[(size_t)m * N + n] = out;
+            }
+        }
     }
     ST_TR(6);
 }
@@ -934,7 +990,6 @@ constexpr size_t kChunkLdsBudget = 150 * 1024;  // one workgroup per CU
 constexpr int kSplitTiles = 4;  // CHK split-K: tiles per workgroup
 constexpr int kSplitTilesPerCu = 1;  // CHK: split K when the grid has at most this many tiles per CU
 constexpr int kSplitMinUnits1 = 48;  // CHK, one token block: split only K of at least this many groups
-constexpr int kMaxKSplit = 16;  // CHK split-K: most K slices
 
 template <int FMT, int NSRC, int XM, int MB, int SPU, bool PERM>
 int launch_t(st_context *ctx, Params &p) {
@@ -997,8 +1052,20 @@ int launch_t(st_context *ctx, Params &p) {
                 p.wave_lds = (int)region;
                 p.ksplit = ks;
                 p.part = ks > 1 ? ctx->ws : nullptr;
+                // the reduction fused into the kernel (one counter per tile
+                // group) for up to 8 tokens: graph replay, configs[4] down at 4
+                // tokens 9.8 -> 8.9 us, Llama-7B down 11.9 -> 10.9, o and down at
+                // 8 tokens 0.3-0.8 us faster; at 16 tokens the last slice's
+                // reads (4 token blocks) cost more than the reduce launch
+                // (0.2-0.6 us slower). Not when the context has no counters or
+                // the setting asks for the reduce kernel.
+                const int fuse_dflt = MB <= 2 ? 0 : 1;
+                p.cnt = (ks > 1 && ctx->split_counters && grid <= kSplitCounters &&
+                         !tune(ctx, ST_TUNE_SPLIT_REDUCE_KERNEL, fuse_dflt))
+                            ? ctx->split_counters
+                            : nullptr;
                 if (int rc = launch_kernel<FMT, NSRC, XM, MB, SPU, PERM, 3>(ctx, p, lds)) return rc;
-                if (ks == 1) return ST_OK;
+                if (ks == 1 || p.cnt) return ST_OK;
                 const int mn = p.M * p.N;
                 hipLaunchKernelGGL((split_reduce_kernel<NSRC, is_i8(FMT)>), dim3((mn + 255) / 256), dim3(256), 0,
                                    ctx->stream, p.part, p.scale8, p.y, p.M, p.N, ks);

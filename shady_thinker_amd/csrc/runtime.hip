@@ -89,6 +89,16 @@ int st_context_create(int device, st_context **out) {
         return st::hip_fail(e, "st_context_create: workspace");
     }
     ctx->ws_bytes = kDefaultWorkspace;
+    e = hipMalloc(&ctx->split_counters, st::kSplitCounters * sizeof(unsigned));
+    if (e == hipSuccess) e = hipMemset(ctx->split_counters, 0, st::kSplitCounters * sizeof(unsigned));
+    if (e == hipSuccess) e = hipDeviceSynchronize();
+    if (e != hipSuccess) {
+        if (ctx->split_counters) (void)hipFree(ctx->split_counters);
+        (void)hipFree(ctx->ws);
+        (void)hipStreamDestroy(ctx->stream);
+        delete ctx;
+        return st::hip_fail(e, "st_context_create: split-K counters");
+    }
     *out = ctx;
     st::clear_error();
     return ST_OK;
@@ -145,6 +155,7 @@ int st_context_destroy(st_context *ctx) {
     (void)hipSetDevice(ctx->device);
     (void)hipStreamSynchronize(ctx->stream);
     if (ctx->ws) (void)hipFree(ctx->ws);
+    if (ctx->split_counters) (void)hipFree(ctx->split_counters);
     if (ctx->own_stream) (void)hipStreamDestroy(ctx->stream);
     delete ctx;
     return ST_OK;

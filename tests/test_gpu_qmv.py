@@ -523,8 +523,10 @@ def test_int8_tiled_equals_row_major(gpu, orc, Mr, tune):
 ])
 def test_multi_token_split_k(gpu, orc, kind, K, N, Mr, tune):
     """Fewer 16-column tiles than CUs, several tokens: K is split across
-    workgroups (f32 partials in the workspace, a fixed-order reduce that
-    applies the epilogue). Same values as without the split and as the
+    workgroups (f32 partials in the workspace; the last slice of each tile
+    group to finish adds them in slice order and applies the epilogue, bit
+    for bit what a separate reduce kernel gives, call after call). Same
+    values as without the split and as the
     per-wave fallback, up to f32 summation order; the f64 oracle's bar."""
     def run():
         y = torch.empty(Mr, N, device="cuda")
@@ -553,6 +555,13 @@ def test_multi_token_split_k(gpu, orc, kind, K, N, Mr, tune):
             ref = orc.silu_gate_f64(ref, u)
     x = torch.from_numpy(c["x"]).cuda()
     y = run()
+    tune(SPLIT_REDUCE_KERNEL=0)  # the reduction fused (the default up to 8 tokens)
+    y_fused = run()
+    y_again = run()  # the fused reduction's counters cleared themselves
+    tune(SPLIT_REDUCE_KERNEL=1)  # the same slices reduced by a kernel of their own: same order, same bits
+    y_kernel = run()
+    tune(SPLIT_REDUCE_KERNEL=-1)
+    assert np.array_equal(y_fused, y_again) and np.array_equal(y_fused, y_kernel) and np.array_equal(y, y_kernel)
     tune(NO_KSPLIT=1)
     y1 = run()
     tune(NO_CHUNK=1)
