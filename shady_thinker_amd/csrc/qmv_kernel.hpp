@@ -1013,8 +1013,9 @@ int launch_t(st_context *ctx, Params &p) {
         // blocks split up to 2 tiles per CU, qkv 18.4 -> 16.7 us at 16)
         const int split_max = tune(ctx, ST_TUNE_SPLIT_TILES_CU, MB >= 4 ? 2 : kSplitTilesPerCu);
         const bool split = tiles_cu <= split_max && (MB > 1 || p.units >= kSplitMinUnits1);
-        // (one token: the split's reduce launch costs more than it saves,
-        // configs[4] down 7.2 -> 9.2 us)
+        // (one token: the split costs more than it saves, configs[4] down
+        // 7.2 -> 9.2 us with the reduce launch, 6.75 -> 8.8 us with the
+        // reduction fused)
         if (p.M > 1 && (MB > 1 || split) && !tune(ctx, ST_TUNE_NO_CHUNK, 0)) {
             int grid, tpw, ks = 1;
             if (!split) {
