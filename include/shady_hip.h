@@ -274,6 +274,18 @@ int st_gptq_i4_silu_gemm(st_context *ctx, const uint16_t *gate, const uint16_t *
 int st_int8_matvec(st_context *ctx, const void *x, int x_dtype, const int8_t *w,
                    const float *scale, float *y, int M, int K, int N, uint32_t flags);
 
+/* INT8 prefill GEMM (W8A16): C[M, N] = A[M, K] . (w[N, K]^T * scale[N]),
+ * A f16 row-major, C f32 or f16 (c_dtype). No reference counterpart: the
+ * north star's INT8 GEMM for prefill, the M-token form of st_int8_matvec
+ * for M above its 32 (the reference prefills token by token through the
+ * matvec, src/inference.rs:93-95). Every product is exact in f32 (int8 and
+ * f16 are exact in f16), the sums are f32, the channel scale is applied once
+ * per output. K % 128 == 0, N % 4 == 0; a and w 16-byte aligned; flags:
+ * ST_FLAG_TILED for st_int8_repack's layout. Small grids split K across
+ * workgroups (f32 partials in the context workspace, added in a fixed order). */
+int st_int8_gemm(st_context *ctx, const uint16_t *a, const int8_t *w, const float *scale, void *c,
+                 int c_dtype, int M, int K, int N, uint32_t flags);
+
 /* Upload-time INT8 repack (no reference counterpart): row-major w[N, K] ->
  * tiles of 16 rows in which, per 128-k group, each of a wave's 64 lanes
  * holds 32 contiguous bytes, so the kernel reads 2 KiB contiguous per group.

@@ -1,5 +1,5 @@
-// Prefill GEMM on gfx950: C[M, N] = A[M, K] (f16) . dequant(W), W GPTQ int4.
-// No reference counterpart: the reference prefills token by token through
+// Prefill GEMM on gfx950: C[M, N] = A[M, K] (f16) . dequant(W), W GPTQ int4
+// or INT8 (per-output-channel scale). No reference counterpart: the reference prefills token by token through
 // the matvec (src/inference.rs:93-95). Dequant semantics are the reference's
 // ((q - z) * s, src/shaders/gptq_matvec.wgsl:51-58):
 //
@@ -31,6 +31,12 @@
 //    reduce kernel).
 //  * Act-order: K is sorted by group at upload (st_gptq_i4_act_order); the
 //    matching column gather of A is part of the pre-pass.
+//  * INT8 (st_int8_gemm, W8A16): a lane's B fragment is 8 consecutive k of
+//    one weight row, so A needs no reordering and the tiles are DMA'd from
+//    the caller's buffer (no pre-pass). Bytes -> f16: xor 0x80, v_perm each
+//    byte under the f16 exponent of 1024 (1024 + b + 128), one packed add of
+//    -1152: exact. Every product int8 x f16 is exact in f32, so only the f32
+//    sums round; the channel scale multiplies C once in the epilogue.
 #include "common.hpp"
 
 #include <algorithm>
@@ -96,13 +102,32 @@ __device__ __forceinline__ half8 word_to_b(unsigned w, const BConv &c) {
     return __builtin_bit_cast(half8, r);
 }
 
+// 8 int8 weights (two words, k0..k7) -> the f16 B fragment in k order:
+// (b ^ 0x80) under the exponent byte 0x64 is 1024 + 128 + b, minus 1152.
+__device__ __forceinline__ half8 bytes_to_b(unsigned w0, unsigned w1) {
+    const unsigned e = 0x64646464u;
+    const half2_t off = {(_Float16)-1152.0f, (_Float16)-1152.0f};
+    w0 ^= 0x80808080u;
+    w1 ^= 0x80808080u;
+    const half2_t h0 = __builtin_bit_cast(half2_t, __builtin_amdgcn_perm(e, w0, 0x04010400u)) + off;
+    const half2_t h1 = __builtin_bit_cast(half2_t, __builtin_amdgcn_perm(e, w0, 0x04030402u)) + off;
+    const half2_t h2 = __builtin_bit_cast(half2_t, __builtin_amdgcn_perm(e, w1, 0x04010400u)) + off;
+    const half2_t h3 = __builtin_bit_cast(half2_t, __builtin_amdgcn_perm(e, w1, 0x04030402u)) + off;
+    const u32x4 r = {__builtin_bit_cast(unsigned, h0), __builtin_bit_cast(unsigned, h1), __builtin_bit_cast(unsigned, h2),
+                     __builtin_bit_cast(unsigned, h3)};
+    return __builtin_bit_cast(half8, r);
+}
+
 // CB_ = 32-column MFMA blocks per wave: 2 (workgroup tile 128 x 256) or 1
 // (128 x 128, for grids whose 128 x 256 tiles would leave CUs idle).
-template <int GS, bool TILED, bool F16OUT, int CB_>
+// I8: qw is INT8 w (row-major [N, K] or st_int8_repack's tiles), sc / qz /
+// zoff unused, chs the f32 channel scales.
+template <int GS, bool TILED, bool F16OUT, int CB_, bool I8>
 __global__ __launch_bounds__(kThreads, kWavesPerSimd) void gemm_kernel(const _Float16 *__restrict__ A, const uint32_t *__restrict__ qw,
                                                            const uint16_t *__restrict__ sc, const uint32_t *__restrict__ qz,
-                                                           int zoff, const float *__restrict__ rsc, void *__restrict__ C,
-                                                           int M, int K, int N, int kps, float *__restrict__ part) {
+                                                           int zoff, const float *__restrict__ rsc, const float *__restrict__ chs,
+                                                           void *__restrict__ C, int M, int K, int N, int kps,
+                                                           float *__restrict__ part) {
     constexpr int CB = CB_;            // (hides the namespace-scope defaults)
     constexpr int BN = 32 * CB * WN;
     // Two separate arrays (not one [2][...]) so that alias analysis can tell
@@ -168,11 +193,20 @@ __global__ __launch_bounds__(kThreads, kWavesPerSimd) void gemm_kernel(const _Fl
     //    8 (j / 2) + 2q + j % 2 of the tile and is used at k-step
     //    t = 4 (j / 2) + 2 ql + j % 2, so the tile's first 64 k are steps 0..3
     //    (the group boundary rule is the same for both layouts).
+    //  * INT8: a lane's bytes of a K tile are four 16-byte pieces p, each
+    //    two k-steps (8 k each). Row-major: 64 contiguous bytes of row col
+    //    at k = 64 hi + 16 p. Tiled (one 128-k group per K tile): lane
+    //    block q = 2 hi + p / 2 (32 bytes), half st = p % 2, k = 16 q + 64 st.
     constexpr int WPL = GS / 32;  // tiled: words per lane per group
     int boff[CB];
 #pragma unroll
     for (int cb = 0; cb < CB; ++cb) {
-        if constexpr (TILED) {
+        if constexpr (I8) {
+            if constexpr (TILED)
+                boff[cb] = (((col[cb] >> 4) * (K / KT) * 64 + 32 * hi + (col[cb] & 15)) * 32);
+            else
+                boff[cb] = col[cb] * K + 64 * hi;
+        } else if constexpr (TILED) {
             const int G = K / GS;
             boff[cb] = (((col[cb] >> 4) * G * 64 + 32 * hi + (col[cb] & 15)) * WPL) * 4;
         } else {
@@ -180,13 +214,33 @@ __global__ __launch_bounds__(kThreads, kWavesPerSimd) void gemm_kernel(const _Fl
         }
     }
     // logical 16-byte chunk (8 k) of the A tile that k-step t uses in this lane
-    auto kchunk = [&](int t) { return TILED ? 8 * (t >> 2) + 4 * hi + 2 * ((t >> 1) & 1) + (t & 1) : 2 * t + hi; };
+    auto kchunk = [&](int t) {
+        if constexpr (I8) return TILED ? 8 * ((t >> 1) & 1) + 4 * hi + 2 * (t >> 2) + (t & 1) : 8 * hi + t;
+        return TILED ? 8 * (t >> 2) + 4 * hi + 2 * ((t >> 1) & 1) + (t & 1) : 2 * t + hi;
+    };
 
-    unsigned bw[2][KT / 16][CB];
-    auto load_b = [&](unsigned (&dst)[KT / 16][CB], int kt) {
+    // INT8 keeps one B buffer: piece p of the next K tile is loaded into
+    // the registers of this tile's piece p once both of its k-steps are
+    // converted (GPTQ: the next tile's words go to the other buffer).
+    constexpr int BWN = I8 ? KT / 8 : KT / 16;  // B words per lane per K tile and column block
+    unsigned bw[I8 ? 1 : 2][BWN][CB];
+    auto load_piece = [&](unsigned (&dst)[BWN][CB], int kt, int p) {
 #pragma unroll
         for (int cb = 0; cb < CB; ++cb) {
-            if constexpr (TILED) {
+            const int po = TILED ? (p >> 1) * 16 * 32 + (p & 1) * 16 : 16 * p;
+            const u32x4 w = __builtin_amdgcn_raw_buffer_load_b128(rb_, boff[cb] + po, TILED ? kt * 64 * 32 : kt * KT, 0);
+#pragma unroll
+            for (int j = 0; j < 4; ++j) dst[4 * p + j][cb] = w[j];
+        }
+    };
+    auto load_b = [&](unsigned (&dst)[BWN][CB], int kt) {
+#pragma unroll
+        for (int cb = 0; cb < CB; ++cb) {
+            if constexpr (I8) {
+                if (cb == 0)
+#pragma unroll
+                    for (int p = 0; p < 4; ++p) load_piece(dst, kt, p);
+            } else if constexpr (TILED) {
 #pragma unroll
                 for (int ql = 0; ql < 2; ++ql) {
                     u32x4 w;
@@ -239,6 +293,7 @@ __global__ __launch_bounds__(kThreads, kWavesPerSimd) void gemm_kernel(const _Fl
                                           kRsrcWord3);
     unsigned sraw[2][GPT][CB], zraw[2][GPT][CB];
     auto load_groups = [&](int slot, int kt) {
+        if constexpr (I8) return;
 #pragma unroll
         for (int gi = 0; gi < GPT; ++gi) {
             const int g = (kt * KT) / GS + gi;
@@ -250,6 +305,7 @@ __global__ __launch_bounds__(kThreads, kWavesPerSimd) void gemm_kernel(const _Fl
         }
     };
     auto group_consts = [&](int slot, int gi) {
+        if constexpr (I8) return;
 #pragma unroll
         for (int cb = 0; cb < CB; ++cb) {
             const int z = has_z ? (int)((zraw[slot][gi][cb] >> (4 * (col[cb] & 7))) & 0xF) + zoff : 8;
@@ -282,7 +338,8 @@ __global__ __launch_bounds__(kThreads, kWavesPerSimd) void gemm_kernel(const _Fl
         const int kn = min(kt + 1, kt1 - 1);
         load_groups(BUF ^ 1, kn);
         a_dma(std::integral_constant<int, BUF ^ 1>{}, kn);  // stage BUF ^ 1 was last read before the previous barrier
-        load_b(bw[BUF ^ 1], kn);
+        constexpr int RBUF = I8 ? 0 : BUF;                  // the B buffer this tile reads
+        if constexpr (!I8) load_b(bw[BUF ^ 1], kn);
         // Keep the prefetch here: left alone, the scheduler sinks these loads
         // to the end of the tile (shorter live ranges), where the barrier
         // then waits for their whole latency.
@@ -302,8 +359,12 @@ __global__ __launch_bounds__(kThreads, kWavesPerSimd) void gemm_kernel(const _Fl
         // keeps the matrix and vector units busy together.
         half8 bf[2][CB];
         if ((BUF * KT) % GS == 0) group_consts(BUF, 0);
+        auto to_b = [&](int t, int cb) {
+            if constexpr (I8) return bytes_to_b(bw[RBUF][2 * t][cb], bw[RBUF][2 * t + 1][cb]);
+            return word_to_b(bw[RBUF][t][cb], bc[cb]);
+        };
 #pragma unroll
-        for (int cb = 0; cb < CB; ++cb) bf[0][cb] = word_to_b(bw[BUF][0][cb], bc[cb]);
+        for (int cb = 0; cb < CB; ++cb) bf[0][cb] = to_b(0, cb);
 #pragma unroll
         for (int t = 0; t < KT / 16; ++t) {
             const int cur = t & 1;
@@ -317,7 +378,9 @@ __global__ __launch_bounds__(kThreads, kWavesPerSimd) void gemm_kernel(const _Fl
             if (t + 1 < KT / 16) {
                 if ((BUF * KT + 16 * (t + 1)) % GS == 0) group_consts(BUF, (16 * (t + 1)) / GS);
 #pragma unroll
-                for (int cb = 0; cb < CB; ++cb) bf[cur ^ 1][cb] = word_to_b(bw[BUF][t + 1][cb], bc[cb]);
+                for (int cb = 0; cb < CB; ++cb) bf[cur ^ 1][cb] = to_b(t + 1, cb);
+                if constexpr (I8)
+                    if ((t + 1) & 1) load_piece(bw[0], kn, (t + 1) >> 1);  // piece (t + 1) / 2 is converted
 #pragma unroll
                 for (int i = 0; i < RB * CB; ++i) {
                     __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);                   // one MFMA
@@ -326,7 +389,9 @@ __global__ __launch_bounds__(kThreads, kWavesPerSimd) void gemm_kernel(const _Fl
                 }
             }
         }
-        __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): next tile's A DMAs (and B words) landed
+        // vmcnt(0): the next tile's A DMAs (and GPTQ B words) landed. INT8:
+        // the 4 CB piece loads issued after the DMAs may stay in flight.
+        __builtin_amdgcn_s_waitcnt(I8 ? 0x0F70 + 4 * CB : 0x0F70);
         __syncthreads();
     };
     // K % 256 == 0 when GS == 256 and kps is even, so a group never ends on
@@ -344,12 +409,14 @@ __global__ __launch_bounds__(kThreads, kWavesPerSimd) void gemm_kernel(const _Fl
         for (int cb = 0; cb < CB; ++cb) {
             const int n = nw + 32 * cb + l32;
             if (n >= N) continue;
+            const float cs = I8 ? chs[n] : 1.0f;
 #pragma unroll
             for (int i = 0; i < 16; ++i) {
                 const int m = m0 + mw + rb * 32 + 8 * (i >> 2) + 4 * hi + (i & 3);
                 if (m >= M) continue;
                 // rows the pre-pass scaled down by 2^-e get 2^e back (exact)
-                const float v = rsc ? acc[rb][cb][i] * rsc[m] : acc[rb][cb][i];
+                float v = rsc ? acc[rb][cb][i] * rsc[m] : acc[rb][cb][i];
+                if constexpr (I8) v *= cs;
                 if (part)  // split-K: this split's f32 partial
                     part[((size_t)split * M + m) * N + n] = v;
                 else if constexpr (F16OUT)
@@ -476,26 +543,40 @@ struct Split {
     float *part;  // nullptr when S == 1
 };
 
-template <int GS, bool TILED, int CBL>
-int launch_cb(st_context *ctx, const _Float16 *A, const uint32_t *qw, const uint16_t *sc, const uint32_t *qz, int zoff,
-              const float *rsc, void *C, bool f16out, int M, int K, int N, const Split &sp) {
-    const int T = ((M + BM - 1) / BM) * ((N + 32 * CBL * WN - 1) / (32 * CBL * WN));
+// The GEMM's operands. I8: qw is the INT8 weight, chs its channel scales
+// (sc, qz, zoff unused).
+struct GemmArgs {
+    const _Float16 *A;
+    const uint32_t *qw;
+    const uint16_t *sc;
+    const uint32_t *qz;
+    int zoff;
+    const float *rsc, *chs;
+    void *C;
+    bool f16out;
+    int M, K, N;
+};
+
+template <int GS, bool TILED, int CBL, bool I8>
+int launch_cb(st_context *ctx, const GemmArgs &g, const Split &sp) {
+    const int T = ((g.M + BM - 1) / BM) * ((g.N + 32 * CBL * WN - 1) / (32 * CBL * WN));
     const dim3 grid(T * sp.S);
-    if (f16out)
-        hipLaunchKernelGGL((gemm_kernel<GS, TILED, true, CBL>), grid, dim3(kThreads), 0, ctx->stream, A, qw, sc, qz, zoff,
-                           rsc, C, M, K, N, sp.kps, sp.part);
+    if (g.f16out)
+        hipLaunchKernelGGL((gemm_kernel<GS, TILED, true, CBL, I8>), grid, dim3(kThreads), 0, ctx->stream, g.A, g.qw, g.sc,
+                           g.qz, g.zoff, g.rsc, g.chs, g.C, g.M, g.K, g.N, sp.kps, sp.part);
     else
-        hipLaunchKernelGGL((gemm_kernel<GS, TILED, false, CBL>), grid, dim3(kThreads), 0, ctx->stream, A, qw, sc, qz, zoff,
-                           rsc, C, M, K, N, sp.kps, sp.part);
+        hipLaunchKernelGGL((gemm_kernel<GS, TILED, false, CBL, I8>), grid, dim3(kThreads), 0, ctx->stream, g.A, g.qw, g.sc,
+                           g.qz, g.zoff, g.rsc, g.chs, g.C, g.M, g.K, g.N, sp.kps, sp.part);
     return st::launch_check("gemm_kernel");
 }
 
-template <int GS, bool TILED>
-int launch_gs(st_context *ctx, const _Float16 *A, const uint32_t *qw, const uint16_t *sc, const uint32_t *qz, int zoff,
-              const float *rsc, void *C, bool f16out, int M, int K, int N, int cb, const Split &sp) {
-    const int rc = cb == 1 ? launch_cb<GS, TILED, 1>(ctx, A, qw, sc, qz, zoff, rsc, C, f16out, M, K, N, sp)
-                           : launch_cb<GS, TILED, 2>(ctx, A, qw, sc, qz, zoff, rsc, C, f16out, M, K, N, sp);
+template <int GS, bool TILED, bool I8 = false>
+int launch_gs(st_context *ctx, const GemmArgs &g, int cb, const Split &sp) {
+    const int rc = cb == 1 ? launch_cb<GS, TILED, 1, I8>(ctx, g, sp) : launch_cb<GS, TILED, 2, I8>(ctx, g, sp);
     if (rc) return rc;
+    const int M = g.M, N = g.N;
+    const bool f16out = g.f16out;
+    void *C = g.C;
     if (sp.S > 1) {
         const size_t MN = (size_t)M * N;
         const dim3 rg((unsigned)((MN / 4 + 255) / 256));
@@ -509,12 +590,11 @@ int launch_gs(st_context *ctx, const _Float16 *A, const uint32_t *qw, const uint
 }
 
 template <bool TILED>
-int launch_tiled(st_context *ctx, const _Float16 *A, const uint32_t *qw, const uint16_t *sc, const uint32_t *qz, int zoff,
-                 const float *rsc, void *C, bool f16out, int M, int K, int N, int gs, int cb, const Split &sp) {
+int launch_tiled(st_context *ctx, const GemmArgs &g, int gs, int cb, const Split &sp) {
     switch (gs) {
-        case 64: return launch_gs<64, TILED>(ctx, A, qw, sc, qz, zoff, rsc, C, f16out, M, K, N, cb, sp);
-        case 128: return launch_gs<128, TILED>(ctx, A, qw, sc, qz, zoff, rsc, C, f16out, M, K, N, cb, sp);
-        default: return launch_gs<256, TILED>(ctx, A, qw, sc, qz, zoff, rsc, C, f16out, M, K, N, cb, sp);
+        case 64: return launch_gs<64, TILED>(ctx, g, cb, sp);
+        case 128: return launch_gs<128, TILED>(ctx, g, cb, sp);
+        default: return launch_gs<256, TILED>(ctx, g, cb, sp);
     }
 }
 
@@ -586,13 +666,12 @@ int gemm_impl(const char *fn, st_context *ctx, const uint16_t *a, const uint16_t
     hipLaunchKernelGGL(prep_a_kernel, dim3(M), dim3(256), (size_t)K * sizeof(_Float16), ctx->stream,
                        reinterpret_cast<const _Float16 *>(a), reinterpret_cast<const _Float16 *>(u), perm, A, rsc, K);
     if (int rc = st::launch_check("prep_a_kernel")) return rc;
-    const int zoff = (flags & ST_FLAG_ZEROS_PLUS_ONE) ? 1 : 0;
-    const bool f16out = c_dtype == ST_F16;
+    const GemmArgs g{A, qweight, scales, qzeros, (flags & ST_FLAG_ZEROS_PLUS_ONE) ? 1 : 0, rsc, nullptr, c,
+                     c_dtype == ST_F16, M, K, N};
     const int cb = pick_cb(ctx, M, N);
     const Split sp = plan_split(ctx, M, K, N, cb, need);
-    if (flags & ST_FLAG_TILED)
-        return launch_tiled<true>(ctx, A, qweight, scales, qzeros, zoff, rsc, c, f16out, M, K, N, group_size, cb, sp);
-    return launch_tiled<false>(ctx, A, qweight, scales, qzeros, zoff, rsc, c, f16out, M, K, N, group_size, cb, sp);
+    if (flags & ST_FLAG_TILED) return launch_tiled<true>(ctx, g, group_size, cb, sp);
+    return launch_tiled<false>(ctx, g, group_size, cb, sp);
 }
 
 }  // namespace
@@ -610,4 +689,23 @@ extern "C" int st_gptq_i4_silu_gemm(st_context *ctx, const uint16_t *gate, const
     if (!up) return st::fail(ST_ERR_INVALID, "st_gptq_i4_silu_gemm: NULL argument");
     return gemm_impl("st_gptq_i4_silu_gemm", ctx, gate, up, qweight, scales, qzeros, perm, c, c_dtype, M, K, N,
                      group_size, flags);
+}
+
+extern "C" int st_int8_gemm(st_context *ctx, const uint16_t *a, const int8_t *w, const float *scale, void *c,
+                            int c_dtype, int M, int K, int N, uint32_t flags) {
+    const char *fn = "st_int8_gemm";
+    if (!ctx || !a || !w || !scale || !c) return st::fail(ST_ERR_INVALID, "%s: NULL argument", fn);
+    if (M < 1 || K <= 0 || K % KT || N <= 0 || N % 4)
+        return st::fail(ST_ERR_SHAPE, "%s: M=%d K=%d N=%d (K %% 128, N %% 4)", fn, M, K, N);
+    if (c_dtype != ST_F32 && c_dtype != ST_F16) return st::fail(ST_ERR_INVALID, "%s: c_dtype %d", fn, c_dtype);
+    if (!st::aligned16(a) || !st::aligned16(w)) return st::fail(ST_ERR_ALIGN, "%s: a and w must be 16-byte aligned", fn);
+    const bool tiled = (flags & ST_FLAG_TILED) != 0;
+    const size_t wbytes = tiled ? st_int8_tiled_bytes(K, N) : (size_t)K * N;
+    if ((size_t)M * K * 2 > 0x7FFFFFFFu || wbytes > 0x7FFFFFFFu)
+        return st::fail(ST_ERR_SHAPE, "%s: a or w above 2 GiB (M=%d K=%d N=%d); split M or N", fn, M, K, N);
+    const GemmArgs g{reinterpret_cast<const _Float16 *>(a), reinterpret_cast<const uint32_t *>(w), nullptr, nullptr, 0,
+                     nullptr, scale, c, c_dtype == ST_F16, M, K, N};
+    const int cb = pick_cb(ctx, M, N);
+    const Split sp = plan_split(ctx, M, K, N, cb, 0);
+    return tiled ? launch_gs<128, true, true>(ctx, g, cb, sp) : launch_gs<128, false, true>(ctx, g, cb, sp);
 }

@@ -139,6 +139,20 @@ def int8_matvec(gpu, x, w, scale, y, k: int, n: int, flags: int = 0) -> None:
     call("st_int8_matvec", gpu.handle, ptr(x), _xdtype(x), ptr(w), ptr(scale), ptr(y), m, k, n, flags)
 
 
+def int8_gemm(gpu, a, w, scale, c, k: int, n: int, flags: int = 0) -> None:
+    """c[M, n] = a[M, k] (f16) . (w[n, k]^T * scale[n]): the INT8 prefill
+    GEMM (W8A16 on f16 MFMA), c float32 or float16; flags ST_FLAG_TILED when
+    w is in the layout of st_int8_repack."""
+    torch = _torch()
+    m = _check_io(a, k, c, n, x_dtypes=(torch.float16,), out_dtypes=(torch.float32, torch.float16), name="a")
+    nbytes = lib().st_int8_tiled_bytes(k, n) if flags & ST_FLAG_TILED else k * n
+    _need(w, "w", (torch.int8,), nbytes)
+    _need(scale, "scale", (torch.float32,), n)
+    cd = ST_F32 if c.dtype == torch.float32 else ST_F16
+    gpu.sync_stream()
+    call("st_int8_gemm", gpu.handle, ptr(a), ptr(w), ptr(scale), ptr(c), cd, m, k, n, flags)
+
+
 def gptq_gemm(gpu, a, qweight, scales, c, k: int, n: int, group_size: int = 128, qzeros=None, perm=None,
               flags: int = 0) -> None:
     """c[M, n] = a[M, k] (f16) . dequant(W), c float32 or float16."""
@@ -186,7 +200,8 @@ def bf16_matvec(gpu, x, w, y, k: int, n: int) -> None:
 def linear(gpu, x, w, y) -> None:
     """Dispatch on the weight type: GptqWeight -> st_gptq_i4_matvec (M <= 32)
     or the prefill GEMM (M > 32: it computes on f16 activations, so f32 x is
-    rounded to f16 first); Int8Weight -> st_int8_matvec."""
+    rounded to f16 first); Int8Weight -> st_int8_matvec (M <= 32) or
+    st_int8_gemm (M > 32, likewise on f16 activations)."""
     if isinstance(w, GptqWeight):
         m = _rows(x, w.K)
         if m > 32:
@@ -195,6 +210,11 @@ def linear(gpu, x, w, y) -> None:
         else:
             gptq_matvec(gpu, "linear", x, w.qweight, w.scales, y, w.K, w.N, w.group_size, w.qzeros, w.perm, w.flags)
     elif isinstance(w, Int8Weight):
-        int8_matvec(gpu, x, w.w, w.scale, y, w.K, w.N, w.flags)
+        m = _rows(x, w.K)
+        if m > 32:
+            xa = x if x.dtype == _torch().float16 else x.to(_torch().float16)
+            int8_gemm(gpu, xa, w.w, w.scale, y, w.K, w.N, w.flags)
+        else:
+            int8_matvec(gpu, x, w.w, w.scale, y, w.K, w.N, w.flags)
     else:
         raise TypeError(type(w))

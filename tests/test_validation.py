@@ -105,6 +105,32 @@ def test_int8_and_bf16_reject_short_buffers():
         M.bf16_matvec(NoGpu(), x, torch.zeros(N * K - 1, dtype=torch.int16), y, K, N)
 
 
+def test_int8_gemm_checks_and_linear_routes_it():
+    from shady_thinker_amd.weights import Int8Weight
+
+    w8, sc = torch.zeros(K * N, dtype=torch.int8), torch.zeros(N)
+    a16, c = torch.zeros(48, K, dtype=torch.float16), torch.zeros(48, N)
+    with pytest.raises(ShadyHipError):  # valid: reaches the C ABI (NULL context)
+        M.int8_gemm(NoGpu(), a16, w8, sc, c, K, N)
+    with pytest.raises(TypeError):  # f32 activations
+        M.int8_gemm(NoGpu(), a16.float(), w8, sc, c, K, N)
+    with pytest.raises(TypeError):  # C is f32 or f16
+        M.int8_gemm(NoGpu(), a16, w8, sc, c.to(torch.bfloat16), K, N)
+    with pytest.raises(ValueError):  # C too short
+        M.int8_gemm(NoGpu(), a16, w8, sc, torch.zeros(47, N), K, N)
+    with pytest.raises(ValueError):  # short weight
+        M.int8_gemm(NoGpu(), a16, w8[:-1], sc, c, K, N)
+    with pytest.raises(TypeError):  # f16 channel scales
+        M.int8_gemm(NoGpu(), a16, w8, sc.half(), c, K, N)
+    Kt, Nt = 256, 72  # tiled: K * N bytes are too few
+    with pytest.raises(ValueError):
+        M.int8_gemm(NoGpu(), a16[:, :Kt], torch.zeros(Kt * Nt, dtype=torch.int8), torch.zeros(Nt),
+                    torch.zeros(48, Nt), Kt, Nt, ST_FLAG_TILED)
+    w = Int8Weight(w8, sc, K, N, 0)
+    with pytest.raises(ShadyHipError):  # 48 tokens of f32 x: rounded to f16, then the GEMM call
+        M.linear(NoGpu(), a16.float(), w, c)
+
+
 def test_upload_tensor_checks():
     qw = np.zeros((K // 8, N), np.int32)
     sc = np.zeros((K // GS, N), np.float16)
