@@ -196,7 +196,7 @@ def main():
     ap.add_argument("--copy-calibrate", action="store_true",
                     help="profiling helper: 10 plain 64 MiB device copies (calibrates FETCH_SIZE / WRITE_SIZE)")
     ap.add_argument("--only", default="", help="profiling helper: launch only this kernel, eagerly "
-                                               "(q|gate_up|down|gemm|gemm512|lm_int4), or replay one configs[4] "
+                                               "(q|gate_up|down|gemm|gemm512|int8gemm|lm_int4), or replay one configs[4] "
                                                "stack step per step (stack1|stack16)")
     args = ap.parse_args()
     world = int(os.environ.get("WORLD_SIZE", "1"))
@@ -233,6 +233,21 @@ def main():
         C = torch.empty(Mr, N, device=dev, dtype=torch.float16)
         ms = time_loop(torch, lambda i: Mdl.gptq_gemm(gpu, A, qw, sc, C, K, N, GS, None, perm, sta.ST_FLAG_TILED),
                        args.steps, args.warmup)
+        print(json.dumps({"only": args.only, "M": Mr, "steps": args.steps, "ms_eager": round(ms, 5),
+                          "TFLOP/s": round(2.0 * Mr * K * N / (ms * 1e-3) / 1e12, 1)}))
+        return
+
+    if args.only == "int8gemm":  # eager INT8 prefill GEMM loop (configs[2] weight, M = 2048) for the profiler
+        K, N, Mr = 5120, 13824, 2048
+        w = torch.randint(-127, 128, (N, K), device=dev, dtype=torch.int8, generator=gen)
+        wt = torch.empty(sta._lib.lib().st_int8_tiled_bytes(K, N), dtype=torch.int8, device=dev)
+        gpu.sync_stream()
+        sta._lib.call("st_int8_repack", gpu.handle, w.data_ptr(), wt.data_ptr(), K, N)
+        sc = (torch.randn(N, device=dev, generator=gen) * 0.01).abs()
+        A = torch.randn(Mr, K, device=dev, generator=gen).half()
+        C = torch.empty(Mr, N, device=dev, dtype=torch.float16)
+        ms = time_loop(torch, lambda i: Mdl.int8_gemm(gpu, A, wt, sc, C, K, N, sta.ST_FLAG_TILED), args.steps,
+                       args.warmup)
         print(json.dumps({"only": args.only, "M": Mr, "steps": args.steps, "ms_eager": round(ms, 5),
                           "TFLOP/s": round(2.0 * Mr * K * N / (ms * 1e-3) / 1e12, 1)}))
         return
@@ -497,6 +512,21 @@ def bench_int8(torch, dev, gpu, Mdl, gen, args):
         out[f"M{Mr}"] = {"ms": round(ms, 5), "GB/s": round(b / (ms * 1e-3) / 1e9, 1),
                          "hbm_frac": round(b / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
                          "TOPS": round(2.0 * Mr * K * N / (ms * 1e-3) / 1e12, 2)}
+    # Prefill on the same weight (st_int8_gemm, f16 A and C), M in {512, 2048},
+    # next to torch's f16 GEMM of the same shape (hipBLASLt, dense f16 B).
+    out["prefill"] = {"kernel": "gemm_kernel INT8 (st_int8_gemm)", "peak_TFLOP/s": F16_MFMA_PEAK_TFLOPS}
+    for Mr in (512, 2048):
+        A = torch.randn(Mr, K, device=dev, generator=gen).half()
+        C = torch.empty(Mr, N, device=dev, dtype=torch.float16)
+        iters = max(10, min(50, args.steps // 4))
+        ms = Replayer(torch, lambda i: Mdl.int8_gemm(gpu, A, ws[0], sc, C, K, N, ST_FLAG_TILED), 1).run(iters, 3)
+        tf = 2.0 * Mr * K * N / (ms * 1e-3) / 1e12
+        B16 = torch.randn(N, K, device=dev, generator=gen).half()
+        ms_ref = Replayer(torch, lambda i: torch.matmul(A, B16.t()), 1).run(iters, 3)
+        del B16
+        out["prefill"][f"M{Mr}"] = {"ms": round(ms, 4), "TFLOP/s": round(tf, 1),
+                                    "mfma_frac": round(tf / F16_MFMA_PEAK_TFLOPS, 4),
+                                    "torch_f16_gemm_TFLOP/s": round(2.0 * Mr * K * N / (ms_ref * 1e-3) / 1e12, 1)}
     del ws
     return out
 
