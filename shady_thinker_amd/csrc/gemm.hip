@@ -221,7 +221,8 @@ __global__ __launch_bounds__(kThreads, kWavesPerSimd) void gemm_kernel(const _Fl
 
     // INT8 keeps one B buffer: piece p of the next K tile is loaded into
     // the registers of this tile's piece p once both of its k-steps are
-    // converted (GPTQ: the next tile's words go to the other buffer).
+    // converted, at step 2p + 1 (GPTQ: the next tile's words go to the other
+    // buffer at the start of the tile).
     constexpr int BWN = I8 ? KT / 8 : KT / 16;  // B words per lane per K tile and column block
     unsigned bw[I8 ? 1 : 2][BWN][CB];
     auto load_piece = [&](unsigned (&dst)[BWN][CB], int kt, int p) {
@@ -368,6 +369,16 @@ __global__ __launch_bounds__(kThreads, kWavesPerSimd) void gemm_kernel(const _Fl
 #pragma unroll
         for (int t = 0; t < KT / 16; ++t) {
             const int cur = t & 1;
+            // INT8: piece (t - 1) / 2 of the next K tile, into the registers
+            // its k-steps used here (both converted by step t - 1), pinned at
+            // the top of the step: left alone, the scheduler sank these loads
+            // to the end of the tile, where the next tile's first conversions
+            // then waited for their whole latency.
+            if constexpr (I8)
+                if (t & 1) {
+                    load_piece(bw[0], kn, t >> 1);
+                    __builtin_amdgcn_sched_barrier(0);
+                }
 #pragma unroll
             for (int rb = 0; rb < RB; ++rb) {
 #pragma unroll
@@ -379,8 +390,6 @@ __global__ __launch_bounds__(kThreads, kWavesPerSimd) void gemm_kernel(const _Fl
                 if ((BUF * KT + 16 * (t + 1)) % GS == 0) group_consts(BUF, (16 * (t + 1)) / GS);
 #pragma unroll
                 for (int cb = 0; cb < CB; ++cb) bf[cur ^ 1][cb] = to_b(t + 1, cb);
-                if constexpr (I8)
-                    if ((t + 1) & 1) load_piece(bw[0], kn, (t + 1) >> 1);  // piece (t + 1) / 2 is converted
 #pragma unroll
                 for (int i = 0; i < RB * CB; ++i) {
                     __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);                   // one MFMA
