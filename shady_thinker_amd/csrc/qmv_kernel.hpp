@@ -1216,7 +1216,12 @@ namespace qmv {
 //    39-42 us, 65 -> 43 us at 4 tokens; 8 waves are 1.5-2 us slower);
 //  * one source with 2-4 tokens from 2 tiles per CU on, with 8-wave
 //    workgroups (4096 x 11008: 9.0 / 11.5 / 14.6-15.1 -> 8.7 / 8.8 / 10.0 us
-//    at 2 / 3 / 4 tokens; one token is a tie, 7.9-8.5 us either way).
+//    at 2 / 3 / 4 tokens);
+//  * one GPTQ source with one token from 2.5 tiles per CU on, with 8-wave
+//    workgroups (4096 x 11008, 2.7 tiles per CU: 8.3-8.4 -> 7.8-7.9 us;
+//    4096 x 14336: 9.7-9.9 -> 9.2-9.5 us; 2560 x 9728, 2.4 tiles per CU, is a
+//    tie). INT8 with one token keeps the register-ring kernel below 8 tiles
+//    per CU (configs[2], 3.4 tiles per CU: 16.2 against 16.4-16.5 us).
 // With fewer tiles the register-ring kernel is 0.2-1 us faster (q_proj
 // 4.7 against 5.6, down 7.9 against 8.8, configs[4] o 4.4 against 5.6 and
 // q|k|v, 1.5 tiles per CU, 5.9-6.3 against 6.0-6.5).
@@ -1232,8 +1237,9 @@ int launch_fmt(st_context *ctx, Params &p) {
         const int pick = tune(ctx, ST_TUNE_DECODE_KERNEL, -1);
         const int tiles_cu = (p.ntiles + ncu - 1) / ncu;
         const bool many = NSRC == 1 && tiles_cu >= kStreamMinTilesCu;  // 16-wave workgroups
+        const bool gptq_mid = !is_i8(FMT) && 2 * p.ntiles >= 5 * ncu;  // one GPTQ source, 2.5+ tiles per CU
         const bool auto_stream = NSRC == 2 ? tiles_cu >= kStreamMinTilesCu2
-                                           : (many || (p.M >= 2 && p.ntiles >= kStreamMinTilesCu2 * ncu));
+                                           : (many || gptq_mid || (p.M >= 2 && p.ntiles >= kStreamMinTilesCu2 * ncu));
         const int waves = many ? 16 : 8;
         if (p.M <= 4 && (pick == 1 || (pick < 0 && auto_stream))) {
             int rc = -1;

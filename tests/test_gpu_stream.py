@@ -260,13 +260,14 @@ def test_stream_repeat_launches(gpu, orc, tune, K, N, gs, Mr, zeros, act, f16):
     assert e < TOL and orc.rel_l2(ys[0], y_ring) < 1e-6
 
 
-@pytest.mark.parametrize("Mr", [2, 3, 4])
+@pytest.mark.parametrize("Mr", [1, 2, 3, 4])
 def test_multi_token_routing(gpu, orc, Mr):
     """2-4 tokens on one source with 2+ tiles per CU go to the streaming
     kernel with 8-wave workgroups (three staging rows per wave): GPTQ 4096 x
     11008 (688 tiles) with f32 x, and INT8 configs[2] 5120 x 13824 with f32 x
-    (at 4 tokens its 1280 staging items need the third row). Default
-    routing, every row against the f64 oracle."""
+    (at 4 tokens its 1280 staging items need the third row). One token: the
+    GPTQ shape (2.7 tiles per CU) streams too, INT8 takes the register-ring
+    kernel. Default routing, every row against the f64 oracle."""
     c = orc.gptq_case(360 + Mr, 4096, 11008, 128, zeros=True, M=Mr)
     w = up(gpu, c)
     y = run(gpu, "f32", w, None, c["x"])
