@@ -522,20 +522,29 @@ __global__ __launch_bounds__(256) void prep_a_kernel(const _Float16 *__restrict_
     }
 }
 
+constexpr int kMaxSplit = 8;  // K splits of a small GEMM grid (plan_split)
+
 // C[m, n] = sum over s < S of part[s, m, n] (fixed order: deterministic).
 template <bool F16OUT>
 __global__ __launch_bounds__(256) void splitk_reduce_kernel(const float *__restrict__ part, void *__restrict__ C,
                                                             size_t MN, int S) {
     const size_t i = ((size_t)blockIdx.x * 256 + threadIdx.x) * 4;
     if (i >= MN) return;  // MN % 4 == 0 (N % 8 == 0)
-    float4 a = *reinterpret_cast<const float4 *>(part + i);
-    for (int s = 1; s < S; ++s) {
-        const float4 v = *reinterpret_cast<const float4 *>(part + (size_t)s * MN + i);
-        a.x += v.x;
-        a.y += v.y;
-        a.z += v.z;
-        a.w += v.w;
-    }
+    // All slices' loads first (S <= kMaxSplit), then the adds in slice order:
+    // a loop of load, wait, add paid one memory latency per slice.
+    float4 t[kMaxSplit];
+#pragma unroll
+    for (int s = 0; s < kMaxSplit; ++s)
+        t[s] = s < S ? *reinterpret_cast<const float4 *>(part + (size_t)s * MN + i) : float4{};
+    float4 a = t[0];
+#pragma unroll
+    for (int s = 1; s < kMaxSplit; ++s)
+        if (s < S) {
+            a.x += t[s].x;
+            a.y += t[s].y;
+            a.z += t[s].z;
+            a.w += t[s].w;
+        }
     if constexpr (F16OUT) {
         _Float16 *c = static_cast<_Float16 *>(C) + i;
         c[0] = (_Float16)a.x;
@@ -628,7 +637,7 @@ Split plan_split(st_context *ctx, int M, int K, int N, int cb, size_t ws_used) {
     const int slots = 2 * ctx->num_cus;
     const int ntiles = K / KT;
     if (2 * T > ctx->num_cus || ntiles < 8 || st::tune(ctx, ST_TUNE_GEMM_NO_SPLIT, 0)) return sp;
-    int S = std::min({8, (slots + T - 1) / T, ntiles / 4});
+    int S = std::min({kMaxSplit, (slots + T - 1) / T, ntiles / 4});
     const size_t off = (ws_used + 255) & ~size_t(255);
     while (S > 1 && off + (size_t)S * M * N * sizeof(float) > ctx->ws_bytes) --S;
     if (S <= 1) return sp;

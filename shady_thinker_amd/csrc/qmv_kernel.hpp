@@ -953,12 +953,21 @@ __global__ __launch_bounds__(256) void split_reduce_kernel(const float *__restri
     const int idx = blockIdx.x * 256 + threadIdx.x;
     const int MN = M * N;
     if (idx >= MN) return;
+    // Every slice's load is issued before the first add (a loop of load,
+    // wait, add paid one memory latency per slice); the adds keep slice order.
+    float t[kMaxKSplit][NSRC];
+#pragma unroll
+    for (int s = 0; s < kMaxKSplit; ++s)
+#pragma unroll
+        for (int src = 0; src < NSRC; ++src) t[s][src] = s < S ? part[(size_t)(s * NSRC + src) * MN + idx] : 0.0f;
     float v[NSRC];
 #pragma unroll
     for (int src = 0; src < NSRC; ++src) v[src] = 0.0f;
-    for (int s = 0; s < S; ++s)
 #pragma unroll
-        for (int src = 0; src < NSRC; ++src) v[src] += part[(size_t)(s * NSRC + src) * MN + idx];
+    for (int s = 0; s < kMaxKSplit; ++s)
+        if (s < S)
+#pragma unroll
+            for (int src = 0; src < NSRC; ++src) v[src] += t[s][src];
     float out = v[0];
     if constexpr (NSRC == 2) out = silu_f(v[0]) * v[1];
     if constexpr (I8) out *= scale8[idx % N];
