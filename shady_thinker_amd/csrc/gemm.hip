@@ -127,7 +127,7 @@ __global__ __launch_bounds__(kThreads, kWavesPerSimd) void gemm_kernel(const _Fl
                                                            const uint16_t *__restrict__ sc, const uint32_t *__restrict__ qz,
                                                            int zoff, const float *__restrict__ rsc, const float *__restrict__ chs,
                                                            void *__restrict__ C, int M, int K, int N, int kps,
-                                                           float *__restrict__ part) {
+                                                           float *__restrict__ part, int vec) {
     constexpr int CB = CB_;            // (hides the namespace-scope defaults)
     constexpr int BN = 32 * CB * WN;
     // Two separate arrays (not one [2][...]) so that alias analysis can tell
@@ -411,7 +411,63 @@ __global__ __launch_bounds__(kThreads, kWavesPerSimd) void gemm_kernel(const _Fl
     }
 
     // ------------------------------------------------------------ output
-    // 32 x 32 block: lane l holds column l % 32, rows 8 (i / 4) + 4 (l / 32) + i % 4.
+    // Rows the pre-pass scaled down by 2^-e get 2^e back (exact); INT8 applies
+    // its channel scale here. 32 x 32 block: lane l holds column l % 32, rows
+    // 8 (i / 4) + 4 (l / 32) + i % 4.
+    if (vec) {
+        // Staged through LDS, 32 rows at a time: each wave writes its 32 x 32 CB
+        // block into a region of its own (rows padded by 16 bytes) and reads it
+        // back as 16-byte row chunks, so C is written in whole lines (16 stores
+        // per lane for f16 C instead of 128 2-byte ones). The A tiles are free:
+        // the last K tile ended with a barrier after every wave's last read.
+        // vec: C (or the partials) 16-byte aligned and N a multiple of a chunk.
+        auto staged = [&](auto tag) {
+            using T = decltype(tag);
+            constexpr int WC = 32 * CB;                      // columns of the wave
+            constexpr int PITCH = WC * (int)sizeof(T) + 16;  // bytes per staged row
+            constexpr int EPC = 16 / (int)sizeof(T);         // elements per chunk
+            constexpr int CPR = WC / EPC;                    // chunks per row
+            static_assert(2 * 32 * PITCH <= (int)sizeof(As0), "staging region");
+            char *stg = reinterpret_cast<char *>((wave & 2) ? As1 : As0) + (wave & 1) * 32 * PITCH;
+            T *dst = part ? reinterpret_cast<T *>(part + (size_t)split * M * N) : static_cast<T *>(C);
+            float cs[CB];
+#pragma unroll
+            for (int cb = 0; cb < CB; ++cb) cs[cb] = I8 ? chs[min(nw + 32 * cb + l32, N - 1)] : 1.0f;
+#pragma unroll
+            for (int rb = 0; rb < RB; ++rb) {
+#pragma unroll
+                for (int cb = 0; cb < CB; ++cb)
+#pragma unroll
+                    for (int i = 0; i < 16; ++i) {
+                        const int r = 8 * (i >> 2) + 4 * hi + (i & 3);
+                        float v = rsc ? acc[rb][cb][i] * rsc[min(m0 + mw + rb * 32 + r, M - 1)] : acc[rb][cb][i];
+                        if constexpr (I8) v *= cs[cb];
+                        *reinterpret_cast<T *>(stg + r * PITCH + (32 * cb + l32) * (int)sizeof(T)) = (T)v;
+                    }
+                asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // the wave's block is in LDS
+#pragma unroll
+                for (int q = 0; q < 32 * CPR / 64; ++q) {
+                    const int ch = q * 64 + lane, row = ch / CPR, cc = ch % CPR;
+                    const u32x4 v = *reinterpret_cast<const u32x4 *>(stg + row * PITCH + 16 * cc);
+                    const int m = m0 + mw + rb * 32 + row, n = nw + EPC * cc;
+                    if (m >= M) continue;
+                    if (n + EPC <= N) {
+                        *reinterpret_cast<u32x4 *>(dst + (size_t)m * N + n) = v;
+                    } else {
+                        T e[EPC];
+                        __builtin_memcpy(e, &v, 16);
+                        for (int j = 0; j < EPC && n + j < N; ++j) dst[(size_t)m * N + n + j] = e[j];
+                    }
+                }
+                asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // reads done before the next block's writes
+            }
+        };
+        if (part || !F16OUT)
+            staged(0.0f);
+        else
+            staged((_Float16)0);
+        return;
+    }
 #pragma unroll
     for (int rb = 0; rb < RB; ++rb)
 #pragma unroll
@@ -423,7 +479,6 @@ __global__ __launch_bounds__(kThreads, kWavesPerSimd) void gemm_kernel(const _Fl
             for (int i = 0; i < 16; ++i) {
                 const int m = m0 + mw + rb * 32 + 8 * (i >> 2) + 4 * hi + (i & 3);
                 if (m >= M) continue;
-                // rows the pre-pass scaled down by 2^-e get 2^e back (exact)
                 float v = rsc ? acc[rb][cb][i] * rsc[m] : acc[rb][cb][i];
                 if constexpr (I8) v *= cs;
                 if (part)  // split-K: this split's f32 partial
@@ -575,16 +630,23 @@ struct GemmArgs {
     int M, K, N;
 };
 
+// The staged epilogue needs 16-byte aligned rows: C (or the workspace
+// partials) 16-byte aligned and N a multiple of the elements per 16 bytes.
+int vec_ok(const GemmArgs &g, const Split &sp) {
+    if (sp.part) return g.N % 4 == 0;
+    return st::aligned16(g.C) && g.N % (g.f16out ? 8 : 4) == 0;
+}
+
 template <int GS, bool TILED, int CBL, bool I8>
 int launch_cb(st_context *ctx, const GemmArgs &g, const Split &sp) {
     const int T = ((g.M + BM - 1) / BM) * ((g.N + 32 * CBL * WN - 1) / (32 * CBL * WN));
     const dim3 grid(T * sp.S);
     if (g.f16out)
         hipLaunchKernelGGL((gemm_kernel<GS, TILED, true, CBL, I8>), grid, dim3(kThreads), 0, ctx->stream, g.A, g.qw, g.sc,
-                           g.qz, g.zoff, g.rsc, g.chs, g.C, g.M, g.K, g.N, sp.kps, sp.part);
+                           g.qz, g.zoff, g.rsc, g.chs, g.C, g.M, g.K, g.N, sp.kps, sp.part, vec_ok(g, sp));
     else
         hipLaunchKernelGGL((gemm_kernel<GS, TILED, false, CBL, I8>), grid, dim3(kThreads), 0, ctx->stream, g.A, g.qw, g.sc,
-                           g.qz, g.zoff, g.rsc, g.chs, g.C, g.M, g.K, g.N, sp.kps, sp.part);
+                           g.qz, g.zoff, g.rsc, g.chs, g.C, g.M, g.K, g.N, sp.kps, sp.part, vec_ok(g, sp));
     return st::launch_check("gemm_kernel");
 }
 
