@@ -213,3 +213,24 @@ def test_gemm_long_k(gpu, orc):
     y = run_gemm(gpu, w, c["x"])
     ref = orc.gptq_matvec_f64(c["x"], c["qweight"], c["scales"], K, N, gs, qzeros=c["qzeros"], g_idx=c["g_idx"])
     assert orc.rel_l2(y, ref) < 5e-4
+
+
+@pytest.mark.parametrize("out_dtype", [torch.float32, torch.float16])
+def test_gemm_unaligned_c_matches_aligned(gpu, orc, out_dtype):
+    """C one element past a 16-byte boundary takes the per-element epilogue,
+    an aligned C the epilogue staged through LDS (16-byte row chunks): the
+    same values bit for bit."""
+    Mr, K, N, gs = 130, 1024, 264, 128
+    c = orc.gptq_case(77, K, N, gs, zeros=True, M=Mr, x_dtype=np.float16)
+    w = up(gpu, c)
+    a = torch.from_numpy(c["x"]).to(gpu.device)
+    aligned = torch.empty(Mr, N, dtype=out_dtype, device=gpu.device)
+    base = torch.empty(Mr * N + 1, dtype=out_dtype, device=gpu.device)
+    shifted = base[1:].view(Mr, N)
+    assert shifted.data_ptr() % 16 != 0
+    for cc in (aligned, shifted):
+        M.gptq_gemm(gpu, a, w.qweight, w.scales, cc, K, N, gs, w.qzeros, w.perm, w.flags)
+    torch.cuda.synchronize()
+    assert torch.equal(aligned, shifted)
+    ref = orc.gptq_matvec_f64(c["x"], c["qweight"], c["scales"], K, N, gs, qzeros=c["qzeros"])
+    assert orc.rel_l2(aligned.float().cpu().numpy(), ref) < 5e-4

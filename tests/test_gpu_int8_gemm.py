@@ -63,8 +63,11 @@ def test_int8_gemm_integer_exact(gpu, orc, tiled):
     np.testing.assert_array_equal(y, ref.astype(np.float32))
 
 
-def test_int8_gemm_f16_output_and_layouts_agree(gpu, orc):
-    Mr, K, N = 300, 1536, 776
+@pytest.mark.parametrize("N", [776, 388])
+def test_int8_gemm_f16_output_and_layouts_agree(gpu, orc, N):
+    """f16 C equals the f32 C rounded, in both epilogues: rows staged through
+    LDS as 16-byte chunks (N % 8 == 0) and per-element stores (N = 388)."""
+    Mr, K = 300, 1536
     c = orc.int8_case(9, K, N, M=Mr)
     wt = sta.Int8Weight.upload(gpu, c["w"], c["scale"], tiled=True)
     wr = sta.Int8Weight.upload(gpu, c["w"], c["scale"], tiled=False)
