@@ -179,7 +179,11 @@ __global__ __launch_bounds__(kThreads) void i4mm_kernel(const void *__restrict__
     __shared__ float ps0[F32X ? KCU * 16 : 1];  // 2^e per (unit, token) of the chunk in xs0 / xs1
     __shared__ float ps1[F32X ? KCU * 16 : 1];
 
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    // The wave index through readfirstlane: the compiler takes tid >> 6 as
+    // divergent, and the source chosen from it (gate or up) then put the
+    // weight, scale and zero resources in VGPRs, every load of them in a
+    // waterfall loop.
+    const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int t0 = (int)((long long)blockIdx.x * ntiles / gridDim.x);
     const int t1 = (int)((long long)(blockIdx.x + 1) * ntiles / gridDim.x);
     const int tb = wave / (NSRC * S), src = (wave / S) % NSRC, slice = wave % S;
