@@ -109,13 +109,26 @@ class GptqWeight:
     @classmethod
     def upload(cls, gpu, qweight: np.ndarray, scales: np.ndarray, group_size: int = 128,
                qzeros: np.ndarray | None = None, g_idx: np.ndarray | None = None,
-               zeros_plus_one: bool = False, tiled: bool = True) -> "GptqWeight":
+               zeros_plus_one: bool = False, tiled: bool = True,
+               drop_symmetric_zeros: bool = True) -> "GptqWeight":
         """Upload the checkpoint tensors verbatim (src/weights.rs:398); for an
         act-order g_idx, sort rows by group on the device; with `tiled`,
         repack qweight into the decode kernels' tiled layout (values
-        unchanged); otherwise keep the [K/8, N] reference layout."""
+        unchanged); otherwise keep the [K/8, N] reference layout.
+
+        Symmetric checkpoints store every zero point as 8 (7 in the AutoGPTQ
+        v1 z - 1 convention): with `drop_symmetric_zeros` such qzeros are not
+        uploaded, and the kernels use their implicit z = 8, which is the
+        reference's own convention (it never reads qzeros,
+        src/weights.rs:372-374). The dequantized values are the same bit for
+        bit; the decode kernels skip the zero-point table they would
+        otherwise build before their first weight load."""
         torch = gpu.torch
         qw, sc, qzeros, g_idx = check_gptq_tensors(qweight, scales, group_size, qzeros, g_idx)
+        if drop_symmetric_zeros and qzeros is not None:
+            z = np.ascontiguousarray(qzeros).view(np.uint32)
+            if np.all(z == (0x77777777 if zeros_plus_one else 0x88888888)):
+                qzeros, zeros_plus_one = None, False
         K, N = qw.shape[0] * 8, qw.shape[1]
         d_qw = gpu.upload_array(qw.view(np.int32), torch.int32)
         d_sc = gpu.upload_array(sc.view(np.float16), torch.float16)

@@ -18,6 +18,7 @@ def test_loaded_weights_match_oracle(gpu, orc, tmp_path):
     linears, bf16 = load_gptq_checkpoint(gpu, str(tmp_path))
     q = linears["model.layers.0.self_attn.q_proj"]
     assert q.perm is None and q.tiled  # identity g_idx dropped
+    assert q.qzeros is None  # symmetric v1 zeros (every stored 7 + 1 = 8) are the implicit z = 8
     x = torch.from_numpy(src["q"]["x"]).cuda()[None]
     y = torch.empty(1, 64, device="cuda")
     sta.linear(gpu, x, q, y)
@@ -27,7 +28,7 @@ def test_loaded_weights_match_oracle(gpu, orc, tmp_path):
     assert np.array_equal(ref, ref8)  # stored 7 + 1 = the reference's z = 8
     assert orc.rel_l2(y.cpu().numpy()[0], ref) < 1e-6
     d = linears["model.layers.0.mlp.down_proj"]
-    assert d.perm is not None
+    assert d.perm is not None and d.qzeros is not None  # random zeros are kept
     dn = src["down"]
     xd = torch.from_numpy(dn["x"]).cuda()[None]
     yd = torch.empty(1, 32, device="cuda")

@@ -115,6 +115,36 @@ def test_zero_points(gpu, orc, plus_one):
     assert orc.rel_l2(y, ref) < TOL
 
 
+@pytest.mark.parametrize("plus_one", [False, True])
+def test_symmetric_zeros_not_uploaded(gpu, orc, plus_one):
+    """qzeros that are all 8 (all 7 with the v1 +1 convention) are dropped at
+    upload: the kernels' implicit z = 8 gives the same bits as the explicit
+    table (matvec, gate/up and the GEMM), and the oracle's result."""
+    K, N, gs = 2048, 1024, 128
+    c = orc.gptq_case(44, K, N, gs, M=3)
+    z = np.full((K // gs, N // 8), 0x77777777 if plus_one else 0x88888888, np.uint32)
+    kw = dict(zeros_plus_one=plus_one)
+    w_drop = sta.GptqWeight.upload(gpu, c["qweight"], c["scales"], gs, qzeros=z, **kw)
+    w_keep = sta.GptqWeight.upload(gpu, c["qweight"], c["scales"], gs, qzeros=z, drop_symmetric_zeros=False, **kw)
+    assert w_drop.qzeros is None and w_keep.qzeros is not None
+    y_drop, y_keep = run_matvec(gpu, w_drop, c["x"]), run_matvec(gpu, w_keep, c["x"])
+    assert np.array_equal(y_drop, y_keep)
+    ref = orc.gptq_matvec_f64(c["x"], c["qweight"], c["scales"], K, N, gs, qzeros=z, zero_offset=int(plus_one))
+    assert orc.rel_l2(y_drop, ref) < TOL
+    x = torch.from_numpy(c["x"]).cuda()
+    outs = []
+    for w in (w_drop, w_keep):
+        g = torch.empty(3, N, device="cuda")
+        M.fused_gate_up_silu(gpu, x, w.qweight, w.scales, w.qweight, w.scales, g, K, N, gs, w.qzeros, w.qzeros,
+                             None, w.flags)
+        a = torch.randn(48, K, generator=torch.Generator().manual_seed(1)).half().cuda()
+        cg = torch.empty(48, N, device="cuda")
+        M.gptq_gemm(gpu, a, w.qweight, w.scales, cg, K, N, gs, w.qzeros, None, w.flags)
+        torch.cuda.synchronize()
+        outs.append((g.cpu(), cg.cpu()))
+    assert torch.equal(outs[0][0], outs[1][0]) and torch.equal(outs[0][1], outs[1][1])
+
+
 def test_act_order(gpu, orc):
     K, N, gs = 4096, 2048, 128
     c = orc.gptq_case(51, K, N, gs, zeros=True, act_order=True)
