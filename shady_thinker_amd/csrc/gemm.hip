@@ -683,11 +683,15 @@ int launch_tiled(st_context *ctx, const GemmArgs &g, int gs, int cb, const Split
 
 // 32-column blocks per wave: 1 (128 x 128 tiles) when 128 x 256 tiles would
 // give at most one workgroup per CU (then two waves per SIMD instead of
-// one); ST_TUNE_GEMM_CB forces 1 or 2.
-int pick_cb(st_context *ctx, int M, int N) {
+// one); ST_TUNE_GEMM_CB forces 1 or 2. INT8 keeps the wide tiles down to
+// half a workgroup per CU (configs[2]'s weight: M = 512, 216 wide tiles,
+// 85 -> 76-78 us; M = 384, 162 tiles, 72-74 -> 69 us; at M = 256, 108
+// tiles, the narrow ones win).
+int pick_cb(st_context *ctx, int M, int N, bool i8) {
     const int f = st::tune(ctx, ST_TUNE_GEMM_CB, 0);
     if (f == 1 || f == 2) return f;
     const int T2 = ((M + BM - 1) / BM) * ((N + BN - 1) / BN);
+    if (i8) return 2 * T2 >= ctx->num_cus ? 2 : 1;
     return T2 <= ctx->num_cus ? 1 : 2;
 }
 
@@ -751,7 +755,7 @@ int gemm_impl(const char *fn, st_context *ctx, const uint16_t *a, const uint16_t
     if (int rc = st::launch_check("prep_a_kernel")) return rc;
     const GemmArgs g{A, qweight, scales, qzeros, (flags & ST_FLAG_ZEROS_PLUS_ONE) ? 1 : 0, rsc, nullptr, c,
                      c_dtype == ST_F16, M, K, N};
-    const int cb = pick_cb(ctx, M, N);
+    const int cb = pick_cb(ctx, M, N, false);
     const Split sp = plan_split(ctx, M, K, N, cb, need);
     if (flags & ST_FLAG_TILED) return launch_tiled<true>(ctx, g, group_size, cb, sp);
     return launch_tiled<false>(ctx, g, group_size, cb, sp);
@@ -788,7 +792,7 @@ extern "C" int st_int8_gemm(st_context *ctx, const uint16_t *a, const int8_t *w,
         return st::fail(ST_ERR_SHAPE, "%s: a or w above 2 GiB (M=%d K=%d N=%d); split M or N", fn, M, K, N);
     const GemmArgs g{reinterpret_cast<const _Float16 *>(a), reinterpret_cast<const uint32_t *>(w), nullptr, nullptr, 0,
                      nullptr, scale, c, c_dtype == ST_F16, M, K, N};
-    const int cb = pick_cb(ctx, M, N);
+    const int cb = pick_cb(ctx, M, N, true);
     const Split sp = plan_split(ctx, M, K, N, cb, 0);
     return tiled ? launch_gs<128, true, true>(ctx, g, cb, sp) : launch_gs<128, false, true>(ctx, g, cb, sp);
 }
