@@ -205,11 +205,7 @@ __global__ __launch_bounds__(64 * NW) void qmv_stream_kernel(Params p) {
             if constexpr (is_i8(FMT)) {
                 meta[src][d] = __builtin_amdgcn_raw_buffer_load_b32(rs0, vlane_s, soff, 0);
             } else {
-#ifdef ST_PROBE_NOSCALE
-                meta[src][d] = __builtin_amdgcn_raw_buffer_load_b16(src == 0 ? rs0 : rs1, 0u, 0u, 0);
-#else
                 meta[src][d] = __builtin_amdgcn_raw_buffer_load_b16(src == 0 ? rs0 : rs1, vlane_s, soff, 0);
-#endif
                 if constexpr (HZ) zw[src][d] = __builtin_amdgcn_raw_buffer_load_b32(src == 0 ? rz0 : rz1, vlane_z, zoff, 0);
             }
         }
@@ -317,14 +313,6 @@ __global__ __launch_bounds__(64 * NW) void qmv_stream_kernel(Params p) {
 #pragma unroll
         for (int st = 0; st < SPU; ++st) asm volatile("" : "+v"(A[st]));
         asm volatile("" : "+v"(es));
-#ifdef ST_PROBE_NOCOMPUTE
-#pragma unroll
-        for (int src = 0; src < NSRC; ++src)
-            tot[src] += __builtin_bit_cast(float, (w[src][0] ^ A[0].x ^ es.x ^ meta[src][d]) & 0x3FFFFFu);
-        if (false) {
-#else
-        {
-#endif
         v4i acc[NSRC];
 #pragma unroll
         for (int src = 0; src < NSRC; ++src) {
@@ -358,7 +346,6 @@ __global__ __launch_bounds__(64 * NW) void qmv_stream_kernel(Params p) {
             const int hi = S.x + __mul24(z, nh);
             const int lo = (S.y << 8) + S.z + __mul24(z, nl);
             tot[src] = fmaf(fmaf((float)hi, 65536.0f, (float)lo), f, tot[src]);
-        }
         }
         // end of a tile, or of this wave's range (a scalar test): full tiles
         // go out, partial ones to LDS (slot 0: the tile began before this
