@@ -31,7 +31,7 @@
  *  - No call allocates. The context's workspace (st_context_reserve_workspace)
  *    holds the prefill GEMM's pre-processed A and split-K partials, the
  *    split-K partials of multi-token (M > 1) decode calls on linears with few
- *    16-column tiles, and the split f32 x of 12-16-token GPTQ calls on wide
+ *    16-column tiles, and the split f32 x of 9-16-token GPTQ calls on wide
  *    linears; one-token decode calls use none. Calls on one context
  *    are ordered by its stream, so they never overlap on it.
  */
@@ -156,8 +156,8 @@ int st_flush(st_context *ctx);
  * Requires K % group_size == 0, group_size in {64, 128, 256}, N % 8 == 0,
  * 1 <= M <= 32, 16-byte aligned qweight and x. Accumulation: exact integer
  * products of the nibbles with a 3 x 8-bit split of x scaled by a power of
- * two per group, f32 across groups (rel-L2 vs f64 ~1e-7). For 12-16 tokens
- * (per 16-token block) on tiled weights without perm, when N has more
+ * two per group, f32 across groups (rel-L2 vs f64 ~1e-7). For 9-16 tokens
+ * (per 16-token block) on tiled weights, with or without perm, when N has more
  * 16-column tiles than the GPU has CUs: f16 MFMA on exact (q - z) and x (f16
  * x as is; f32 x split once into two f16 parts per 128 k, by a pre-pass that
  * uses the context workspace), f32 sums, rel-L2 vs f64 ~1e-7. The same rule

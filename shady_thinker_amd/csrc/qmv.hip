@@ -70,8 +70,10 @@ __global__ __launch_bounds__(256) void repack8_kernel(const int8_t *__restrict__
 // without act-order, f32 or f16 x) from this many tokens on, when N has more
 // 16-column tiles than the GPU has CUs (as measured on configs[4]'s shapes:
 // at 16 tokens q|k|v 12.0 -> 10.7 us, gate/up 20.2 -> 17.4, lm_head 134 -> 75;
-// with fewer tiles or tokens the integer-limb kernels are faster).
-constexpr int kI4mmMinM = 12;
+// from 9 tokens on (three 4-token blocks for the limb kernels) Llama-7B gate/up
+// 26.5 -> 23.2 us, configs[4] q|k|v 11.5 -> 10.4 and gate/up 18.1 -> 16.2;
+// with fewer tiles, or at 2-8 tokens, the integer-limb kernels are faster).
+constexpr int kI4mmMinM = 9;
 
 bool use_i4mm(const st_context *ctx, const QmvParams &p, bool tiled, int xm) {
     const int ntiles = (p.N + kTileN - 1) / kTileN;

@@ -10,7 +10,7 @@ the same calls for a block of tokens:
 * `decode` (1-32 tokens, f32 activations): q|k|v as one concatenated linear,
   o, gate/up fused into h = silu(x.Wg) * (x.Wu), down on h; every call one
   decode entry point (matvec kernels, or the f16-MFMA skinny kernel for
-  12-16 tokens on wide linears).
+  9-16 tokens on wide linears).
 * `prefill` (any number of tokens, f16 activations): the same projections
   through the prefill GEMM, with the down projection on silu(gate) * up
   fused into the GEMM's A pre-pass (`st_gptq_i4_silu_gemm`).

@@ -832,7 +832,7 @@ def test_int4_mm_f16(gpu, orc, Mr, K, N, gs, zeros, f16, dual, tune):
     (13, 1536, 5200, 256, False, True, True),    # gate/up, f16 x, group 256
 ])
 def test_int4_mm_f16_act_order(gpu, orc, Mr, K, N, gs, zeros, f16, dual, tune):
-    """Act-order checkpoints on the f16-MFMA kernel (12-16 tokens): x read
+    """Act-order checkpoints on the f16-MFMA kernel (9-16 tokens): x read
     through the upload's permutation (rows sorted by group), against the f64
     oracle with scale[g_idx[k]], and against the integer-limb kernels."""
     _force_i4mm(tune)
@@ -858,6 +858,43 @@ def test_int4_mm_f16_act_order(gpu, orc, Mr, K, N, gs, zeros, f16, dual, tune):
     assert np.isfinite(y).all() and e < 1e-5
     tune(I4MM_MIN_M=99)
     assert orc.rel_l2(run(), ref) < TOL
+
+
+@pytest.mark.parametrize("Mr,N,dual,want", [
+    (9, 4112, False, True),     # 257 tiles, 9 tokens: the f16-MFMA kernel
+    (11, 4112, True, True),     # gate/up at 11 tokens
+    (8, 4112, False, False),    # 8 tokens: the limb kernels
+    (10, 4096, False, False),   # 256 tiles, not more than the CUs: the limb kernels
+])
+def test_int4_mm_f16_default_routing(gpu, orc, Mr, N, dual, want, tune):
+    """Which kernel the GPTQ entry points pick by default on an MI355X (256
+    CUs): the f16-MFMA kernel from 9 tokens on linears with more 16-column
+    tiles than CUs, the integer-limb kernels otherwise. The default call's y
+    must equal, bit for bit, the call with that kernel forced; both are
+    checked against the f64 oracle."""
+    ncu = torch.cuda.get_device_properties(gpu.device).multi_processor_count
+    if ncu != 256:
+        pytest.skip(f"routing thresholds are stated for 256 CUs, this GPU has {ncu}")
+    K, gs = 1024, 128
+    c = orc.gptq_case(190 + Mr, K, N, gs, zeros=True, M=Mr)
+    w = up(gpu, c)
+    ref = orc.gptq_matvec_f64(c["x"], c["qweight"], c["scales"], K, N, gs, qzeros=c["qzeros"])
+    if dual:
+        c2 = orc.gptq_case(290 + Mr, K, N, gs, zeros=True)
+        w2 = up(gpu, c2)
+        ref = orc.silu_gate_f64(ref, orc.gptq_matvec_f64(c["x"], c2["qweight"], c2["scales"], K, N, gs,
+                                                         qzeros=c2["qzeros"]))
+        run = lambda: _gate_up(gpu, w, w2, c["x"])
+    else:
+        run = lambda: run_matvec(gpu, w, c["x"], torch.float32)
+    y = run()
+    if want:
+        _force_i4mm(tune)
+    else:
+        tune(I4MM_MIN_M=99)
+    y_forced = run()
+    assert orc.rel_l2(y, ref) < TOL
+    np.testing.assert_array_equal(y, y_forced)
 
 
 def test_int4_mm_f16_integer_exact(gpu, orc, tune):
