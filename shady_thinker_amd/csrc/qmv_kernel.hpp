@@ -994,12 +994,81 @@ int launch_kernel(st_context *ctx, Params &p, size_t lds) {
     return launch_check("qmv_kernel");
 }
 
-constexpr size_t kCoopLdsBudget = 96 * 1024;
+// COOP kernels run one workgroup per CU (one tile each when there are no more
+// tiles than CUs, else a CU's run of tiles), so they may take nearly all of
+// its 160 KiB: two tokens on Llama-7B's down (86 groups, ~100 KiB of staged x)
+// fit only above the former 96 KiB.
+constexpr size_t kCoopLdsBudget = 152 * 1024;
 constexpr size_t kChunkLdsBudget = 150 * 1024;  // one workgroup per CU
 constexpr int kSplitTiles = 4;  // CHK split-K: tiles per workgroup
 constexpr int kSplitTilesPerCu = 1;  // CHK: split K when the grid has at most this many tiles per CU
 constexpr int kSplitMinUnits1 = 48;  // CHK, one token block: split only K of at least this many groups
 constexpr int kLongK12Waves = 8192;  // one-tile GPTQ decode: K from which 12 waves per workgroup beat 16
+
+// The K-chunked cooperative kernel (CM 3) for several tokens: a workgroup
+// per CU owning 2..kMaxTilesPerWg tiles, or (split) groups of kSplitTiles
+// tiles with K split across workgroups. Returns -1 when the shape does not
+// fit it (nothing launched, p unchanged).
+template <int FMT, int NSRC, int XM, int MB, int SPU, bool PERM>
+int launch_chk(st_context *ctx, Params &p, bool split, int ncu, int tiles_cu) {
+    constexpr int IPU = 4 * SPU;
+    int grid, tpw, ks = 1;
+    if (!split) {
+        grid = tiles_cu <= kMaxTilesPerWg ? ncu : (p.ntiles + kMaxTilesPerWg - 1) / kMaxTilesPerWg;
+        tpw = (p.ntiles + grid - 1) / grid;
+    } else {
+        // Fewer tiles than CUs: groups of kSplitTiles tiles share
+        // their x, and K is split into slices so that the grid fills
+        // the CUs (each slice stages only its part of x); f32
+        // partials in the workspace, then split_reduce_kernel.
+        tpw = std::min(kSplitTiles, p.ntiles);
+        grid = (p.ntiles + tpw - 1) / tpw;
+        ks = std::max(1, std::min({ncu / grid, kMaxKSplit, p.units / 2}));
+        if (tune(ctx, ST_TUNE_NO_KSPLIT, 0)) ks = 1;
+        const size_t need = (size_t)ks * NSRC * p.M * p.N * sizeof(float);
+        if (ks > 1 && (need > ctx->ws_bytes || !ctx->ws)) ks = 1;
+    }
+    // compute waves per tile: as many as the waves allow, and no more
+    // than one chunk's staging (kChunkRounds rounds of all waves) covers
+    const int nw = kChunkWaves<NSRC, MB>;
+    const int cap = (int)(64ll * kChunkRounds<NSRC> * nw / ((long long)p.M * IPU * kChunkSlots));
+    const int wpt = std::min(nw / tpw, cap);
+    const int ch = wpt * kChunkSlots;
+    const size_t a_bytes = (size_t)ch * ((size_t)SPU * MB * 4 * p.rb * 16 + (size_t)p.M * 16);
+    const size_t region =
+        (a_bytes + (!is_i8(FMT) ? (size_t)tpw * p.units * NSRC * 16 : 0) + 15) & ~size_t(15);
+    const size_t lds = region + (size_t)nw * NSRC * MB * 64 * sizeof(float);
+    if ((long long)p.ntiles * grid < (1ll << 31) && wpt >= 1 &&
+        (long long)p.M * ch * IPU <= 64ll * kChunkRounds<NSRC> * nw && lds <= kChunkLdsBudget) {
+        p.nwaves = nw;
+        p.tpw = tpw;
+        p.grid = grid * ks;
+        p.chunk = ch;
+        p.nstage = 0;
+        p.wave_lds = (int)region;
+        p.ksplit = ks;
+        p.part = ks > 1 ? ctx->ws : nullptr;
+        // the reduction fused into the kernel (one counter per tile
+        // group) for up to 8 tokens: graph replay, configs[4] down at 4
+        // tokens 9.8 -> 8.9 us, Llama-7B down 11.9 -> 10.9, o and down at
+        // 8 tokens 0.3-0.8 us faster; at 16 tokens the last slice's
+        // reads (4 token blocks) cost more than the reduce launch
+        // (0.2-0.6 us slower). Not when the context has no counters or
+        // the setting asks for the reduce kernel.
+        const int fuse_dflt = MB <= 2 ? 0 : 1;
+        p.cnt = (ks > 1 && ctx->split_counters && grid <= kSplitCounters &&
+                 !tune(ctx, ST_TUNE_SPLIT_REDUCE_KERNEL, fuse_dflt))
+                    ? ctx->split_counters
+                    : nullptr;
+        if (int rc = launch_kernel<FMT, NSRC, XM, MB, SPU, PERM, 3>(ctx, p, lds)) return rc;
+        if (ks == 1 || p.cnt) return ST_OK;
+        const int mn = p.M * p.N;
+        hipLaunchKernelGGL((split_reduce_kernel<NSRC, is_i8(FMT)>), dim3((mn + 255) / 256), dim3(256), 0,
+                           ctx->stream, p.part, p.scale8, p.y, p.M, p.N, ks);
+        return launch_check("split_reduce_kernel");
+    }
+    return -1;
+}
 
 template <int FMT, int NSRC, int XM, int MB, int SPU, bool PERM>
 int launch_t(st_context *ctx, Params &p) {
@@ -1015,72 +1084,26 @@ int launch_t(st_context *ctx, Params &p) {
     // many tiles goes to the single-block kernels below.
     // (up to 16 tokens: calls with more run as 16-token blocks, and 8 token
     // blocks would not fit the registers)
+    bool chk_last = false, split = false;  // the CHK kernel after the COOP one; its K split
+    const int ncu = std::max(1, ctx->num_cus);
+    const int tiles_cu = (p.ntiles + ncu - 1) / ncu;
     if constexpr (MB <= 4 && FMT != FMT_I4) {
-        const int ncu = std::max(1, ctx->num_cus);
-        const int tiles_cu = (p.ntiles + ncu - 1) / ncu;
         // (measured, configs[4] shapes: one token block splits only a long K,
         // down 17 -> 9.8 us at 4 tokens while o_proj, K = 4096, lost; four
         // blocks split up to 2 tiles per CU, qkv 18.4 -> 16.7 us at 16)
         const int split_max = tune(ctx, ST_TUNE_SPLIT_TILES_CU, MB >= 4 ? 2 : kSplitTilesPerCu);
-        const bool split = tiles_cu <= split_max && (MB > 1 || p.units >= kSplitMinUnits1);
+        split = tiles_cu <= split_max && (MB > 1 || p.units >= kSplitMinUnits1);
         // (one token: the split costs more than it saves, configs[4] down
         // 7.2 -> 9.2 us with the reduce launch, 6.75 -> 8.8 us with the
         // reduction fused)
         if (p.M > 1 && (MB > 1 || split) && !tune(ctx, ST_TUNE_NO_CHUNK, 0)) {
-            int grid, tpw, ks = 1;
-            if (!split) {
-                grid = tiles_cu <= kMaxTilesPerWg ? ncu : (p.ntiles + kMaxTilesPerWg - 1) / kMaxTilesPerWg;
-                tpw = (p.ntiles + grid - 1) / grid;
-            } else {
-                // Fewer tiles than CUs: groups of kSplitTiles tiles share
-                // their x, and K is split into slices so that the grid fills
-                // the CUs (each slice stages only its part of x); f32
-                // partials in the workspace, then split_reduce_kernel.
-                tpw = std::min(kSplitTiles, p.ntiles);
-                grid = (p.ntiles + tpw - 1) / tpw;
-                ks = std::max(1, std::min({ncu / grid, kMaxKSplit, p.units / 2}));
-                if (tune(ctx, ST_TUNE_NO_KSPLIT, 0)) ks = 1;
-                const size_t need = (size_t)ks * NSRC * p.M * p.N * sizeof(float);
-                if (ks > 1 && (need > ctx->ws_bytes || !ctx->ws)) ks = 1;
-            }
-            // compute waves per tile: as many as the waves allow, and no more
-            // than one chunk's staging (kChunkRounds rounds of all waves) covers
-            const int nw = kChunkWaves<NSRC, MB>;
-            const int cap = (int)(64ll * kChunkRounds<NSRC> * nw / ((long long)p.M * IPU * kChunkSlots));
-            const int wpt = std::min(nw / tpw, cap);
-            const int ch = wpt * kChunkSlots;
-            const size_t a_bytes = (size_t)ch * ((size_t)SPU * MB * 4 * p.rb * 16 + (size_t)p.M * 16);
-            const size_t region =
-                (a_bytes + (!is_i8(FMT) ? (size_t)tpw * p.units * NSRC * 16 : 0) + 15) & ~size_t(15);
-            const size_t lds = region + (size_t)nw * NSRC * MB * 64 * sizeof(float);
-            if ((long long)p.ntiles * grid < (1ll << 31) && wpt >= 1 &&
-                (long long)p.M * ch * IPU <= 64ll * kChunkRounds<NSRC> * nw && lds <= kChunkLdsBudget) {
-                p.nwaves = nw;
-                p.tpw = tpw;
-                p.grid = grid * ks;
-                p.chunk = ch;
-                p.nstage = 0;
-                p.wave_lds = (int)region;
-                p.ksplit = ks;
-                p.part = ks > 1 ? ctx->ws : nullptr;
-                // the reduction fused into the kernel (one counter per tile
-                // group) for up to 8 tokens: graph replay, configs[4] down at 4
-                // tokens 9.8 -> 8.9 us, Llama-7B down 11.9 -> 10.9, o and down at
-                // 8 tokens 0.3-0.8 us faster; at 16 tokens the last slice's
-                // reads (4 token blocks) cost more than the reduce launch
-                // (0.2-0.6 us slower). Not when the context has no counters or
-                // the setting asks for the reduce kernel.
-                const int fuse_dflt = MB <= 2 ? 0 : 1;
-                p.cnt = (ks > 1 && ctx->split_counters && grid <= kSplitCounters &&
-                         !tune(ctx, ST_TUNE_SPLIT_REDUCE_KERNEL, fuse_dflt))
-                            ? ctx->split_counters
-                            : nullptr;
-                if (int rc = launch_kernel<FMT, NSRC, XM, MB, SPU, PERM, 3>(ctx, p, lds)) return rc;
-                if (ks == 1 || p.cnt) return ST_OK;
-                const int mn = p.M * p.N;
-                hipLaunchKernelGGL((split_reduce_kernel<NSRC, is_i8(FMT)>), dim3((mn + 255) / 256), dim3(256), 0,
-                                   ctx->stream, p.part, p.scale8, p.y, p.M, p.N, ks);
-                return launch_check("split_reduce_kernel");
+            // Two tokens in one block: the one-tile COOP kernel below first
+            // (Llama-7B down 9.8 -> 8.5 us, configs[4] down 8.3 -> 8.1; at 3
+            // tokens they tie), this one when that does not fit
+            if (MB == 1 && p.M == 2) {
+                chk_last = true;
+            } else if (const int rc = launch_chk<FMT, NSRC, XM, MB, SPU, PERM>(ctx, p, split, ncu, tiles_cu); rc != -1) {
+                return rc;
             }
         }
     }
@@ -1133,8 +1156,6 @@ int launch_t(st_context *ctx, Params &p) {
             return launch_kernel<FMT, NSRC, XM, MB, SPU, PERM, 2>(ctx, p, lds);
         };
         if (!tune(ctx, ST_TUNE_NO_COOP, 0)) {
-            const int ncu = std::max(1, ctx->num_cus);
-            const int tiles_cu = (p.ntiles + ncu - 1) / ncu;
             if (tiles_cu >= 2 && !tune(ctx, ST_TUNE_ONE_TILE, 0)) {
                 // more tiles than CUs: a workgroup per CU (all the waves a CU
                 // holds) owns 2..kMaxTilesPerWg tiles and stages x once for them
@@ -1165,6 +1186,9 @@ int launch_t(st_context *ctx, Params &p) {
             }
         }
     }
+    if constexpr (MB <= 4 && FMT != FMT_I4)
+        if (chk_last)
+            if (const int rc = launch_chk<FMT, NSRC, XM, MB, SPU, PERM>(ctx, p, split, ncu, tiles_cu); rc != -1) return rc;
     // fallback: per-wave chunked staging, 4 waves, one tile per workgroup
     const int nw = 4;
     p.nwaves = nw;

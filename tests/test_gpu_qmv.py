@@ -545,6 +545,43 @@ def test_int8_tiled_equals_row_major(gpu, orc, Mr, tune):
     assert orc.rel_l2(ys[0], orc.int8_matvec_f64(c["x"], c["w"], c["scale"], K, N)) < TOL
 
 
+@pytest.mark.parametrize("K,N,zeros,act,silu", [
+    (11008, 4096, False, False, False),  # Llama-7B down: one tile per CU, 86 groups
+    (9728, 2560, True, False, False),    # configs[4] down, zeros
+    (11008, 1000, True, True, False),    # ragged N, act-order
+    (11008, 4096, False, False, True),   # the silu(a) * b form
+])
+def test_two_tokens_long_k(gpu, orc, K, N, zeros, act, silu, tune):
+    """Two tokens on a long K with at most one tile per CU take the one-tile
+    cooperative kernel (the K-split kernel only when that does not fit): its
+    y against the f64 oracle, and against the K-split kernel (forced by
+    switching the cooperative kernels off)."""
+    Mr, gs = 2, 128
+    c = orc.gptq_case(410 + N % 97, K, N, gs, zeros=zeros, act_order=act, M=Mr)
+    w = up(gpu, c)
+    if silu:
+        b = np.random.default_rng(5).standard_normal((Mr, K)).astype(np.float32)
+        h = c["x"] / (1.0 + np.exp(-c["x"].astype(np.float64))) * b
+        ref = orc.gptq_matvec_f64(h, c["qweight"], c["scales"], K, N, gs, qzeros=c["qzeros"], g_idx=c["g_idx"])
+
+        def run():
+            xa = torch.from_numpy(c["x"]).to(gpu.device)
+            xb = torch.from_numpy(b).to(gpu.device)
+            y = torch.empty(Mr, N, device=gpu.device)
+            M.fused_silu_gptq_down(gpu, xa, xb, w.qweight, w.scales, y, K, N, gs, w.qzeros, w.perm, w.flags)
+            torch.cuda.synchronize()
+            return y.cpu().numpy()
+    else:
+        ref = orc.gptq_matvec_f64(c["x"], c["qweight"], c["scales"], K, N, gs, qzeros=c["qzeros"], g_idx=c["g_idx"])
+        run = lambda: run_matvec(gpu, w, c["x"])
+    y = run()
+    tune(NO_COOP=1)
+    y_split = run()
+    print(f"two tokens K={K} N={N}: rel-L2 {orc.rel_l2(y, ref):.3e} (split {orc.rel_l2(y_split, ref):.3e})")
+    assert orc.rel_l2(y, ref) < TOL and orc.rel_l2(y_split, ref) < TOL
+    assert orc.rel_l2(y, y_split) < 1e-6
+
+
 @pytest.mark.parametrize("kind,K,N,Mr", [
     ("gptq", 9728, 2560, 16),   # configs[4] down at batch 16: 160 tiles, K split 6 ways
     ("gptq", 4096, 520, 5),     # 33 tiles, ragged
