@@ -197,7 +197,7 @@ def main():
                     help="profiling helper: 10 plain 64 MiB device copies (calibrates FETCH_SIZE / WRITE_SIZE)")
     ap.add_argument("--only", default="", help="profiling helper: launch only this kernel, eagerly "
                                                "(q|gate_up|down|gemm|gemm512|int8gemm|lm_int4), or replay one configs[4] "
-                                               "stack step per step (stack1|stack16)")
+                                               "stack step per step (stack1|stack16), or its 512-token prefill (prefill512)")
     args = ap.parse_args()
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:
@@ -263,6 +263,10 @@ def main():
         return
     if args.only in ("stack1", "stack16"):  # configs[4] stack: graph replays (per-linear kernel times in the profile)
         out = bench_stack(torch, dev, gpu, Mdl, gen, args, batches=(int(args.only[5:]),), prefill=False)
+        print(json.dumps({"only": args.only, **out}))
+        return
+    if args.only == "prefill512":  # configs[4] 512-token prefill only (per-GEMM times in the profile)
+        out = bench_stack(torch, dev, gpu, Mdl, gen, args, batches=(), prefill=True)
         print(json.dumps({"only": args.only, **out}))
         return
 
@@ -452,9 +456,9 @@ def bench_stack(torch, dev, gpu, Mdl, gen, args, batches=(1, 16), prefill=True):
         torch.cuda.empty_cache()
         return out
     # Prefill of a 512-token prompt through the same weights with the GEMM
-    # (DecoderLinears.prefill: f16 activations and outputs; q|k|v, o, gate,
-    # up, and down on silu(gate) * up fused into the GEMM's A pass), then the
-    # lm_head for the last token only, as a prefill does.
+    # (DecoderLinears.prefill: f16 activations and outputs; q|k|v, o, gate
+    # and up in one call, and down on silu(gate) * up fused into the GEMM's A
+    # pass), then the lm_head for the last token only, as a prefill does.
     P = 512
     xa = torch.randn(P, H, device=dev, generator=gen).half()
     aa = torch.randn(P, Q, device=dev, generator=gen).half()
@@ -474,7 +478,7 @@ def bench_stack(torch, dev, gpu, Mdl, gen, args, batches=(1, 16), prefill=True):
     ms = Replayer(torch, prefill, 1).run(max(3, min(10, args.steps // 20)), 1)
     flops = 2.0 * P * L * (H * Q + 2 * H * KV + Q * H + 2 * H * I + I * H)
     out[f"prefill{P}"] = {"ms": round(ms, 3), "tokens_per_s": round(P / (ms * 1e-3), 1),
-                          "TFLOP/s": round(flops / (ms * 1e-3) / 1e12, 1), "gemm_calls": 5 * L}
+                          "TFLOP/s": round(flops / (ms * 1e-3) / 1e12, 1), "gemm_calls": 4 * L}
     out["weights_GB"] = round(wbytes / 1e9, 3)
     del layers, lm
     torch.cuda.empty_cache()

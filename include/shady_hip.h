@@ -251,6 +251,21 @@ int st_gptq_i4_gemm(st_context *ctx, const uint16_t *a, const uint32_t *qweight,
                     void *c, int c_dtype, int M, int K, int N, int group_size,
                     uint32_t flags);
 
+/* Gate and up projections of one MLP for M tokens in one call:
+ * c_gate = a . dequant(W_gate) and c_up = a . dequant(W_up), both [M, N],
+ * from one pre-processed A and (when no split-K is needed) one launch whose
+ * grid holds the tiles of both weights. The M-token form of the gate/up
+ * half of the reference's MLP (src/model.rs:803-811, the separate gate and
+ * up matvecs it runs one token at a time); st_gptq_i4_silu_gemm then takes
+ * c_gate and c_up for the down projection. Both weights share K, N,
+ * group_size, flags and perm; either may have qzeros or not. Each output is
+ * bit for bit what st_gptq_i4_gemm gives for that weight. */
+int st_gptq_i4_gate_up_gemm(st_context *ctx, const uint16_t *a, const uint32_t *gate_qweight,
+                            const uint16_t *gate_scales, const uint32_t *gate_qzeros,
+                            const uint32_t *up_qweight, const uint16_t *up_scales,
+                            const uint32_t *up_qzeros, const int32_t *perm, void *c_gate, void *c_up,
+                            int c_dtype, int M, int K, int N, int group_size, uint32_t flags);
+
 /* Prefill GEMM on silu(gate) * up: C[M, N] = (silu(gate) * up)[M, K] .
  * dequant(W), gate and up f16 [M, K], silu(v) = v / (1 + exp(-v)) in f32,
  * the product rounded once to f16. The M-token form of

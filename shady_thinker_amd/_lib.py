@@ -74,6 +74,7 @@ _SIGNATURES = {
     "st_gptq_i4_repack": (_I, [_P, _P, _P, _I, _I, _I]),
     "st_gptq_i4_gemm": (_I, [_P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _U32]),
     "st_gptq_i4_silu_gemm": (_I, [_P, _P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _U32]),
+    "st_gptq_i4_gate_up_gemm": (_I, [_P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _U32]),
     "st_bf16_matvec": (_I, [_P, _P, _I, _P, _P, _I, _I, _I]),
     "st_int8_matvec": (_I, [_P, _P, _I, _P, _P, _P, _I, _I, _I, _U32]),
     "st_int8_gemm": (_I, [_P, _P, _P, _P, _P, _I, _I, _I, _I, _U32]),

@@ -127,7 +127,8 @@ __global__ __launch_bounds__(kThreads, kWavesPerSimd) void gemm_kernel(const _Fl
                                                            const uint16_t *__restrict__ sc, const uint32_t *__restrict__ qz,
                                                            int zoff, const float *__restrict__ rsc, const float *__restrict__ chs,
                                                            void *__restrict__ C, int M, int K, int N, int kps,
-                                                           float *__restrict__ part, int vec) {
+                                                           float *__restrict__ part, int vec, const uint32_t *qw1,
+                                                           const uint16_t *sc1, const uint32_t *qz1, void *C1) {
     constexpr int CB = CB_;            // (hides the namespace-scope defaults)
     constexpr int BN = 32 * CB * WN;
     // Two separate arrays (not one [2][...]) so that alias analysis can tell
@@ -142,8 +143,10 @@ __global__ __launch_bounds__(kThreads, kWavesPerSimd) void gemm_kernel(const _Fl
     const int l32 = lane & 31;
     const int hi = lane >> 5;
 
-    // XCD-major tile order: consecutive ids run on the same XCD.
-    const int MT = (M + BM - 1) / BM, NT = (N + BN - 1) / BN;
+    // XCD-major tile order: consecutive ids run on the same XCD. With a
+    // second weight (C1 != NULL: the same A times two [K, N] weights, as the
+    // gate and up projections of an MLP) the N tiles of both form one grid.
+    const int MT = (M + BM - 1) / BM, NT1 = (N + BN - 1) / BN, NT = C1 ? 2 * NT1 : NT1;
     const int T = MT * NT;
     // split-K: workgroup b takes K tiles [kt0, kt1) of tile b % T (kps is
     // even whenever it is not all of K, so a split starts on a group of 256)
@@ -153,7 +156,15 @@ __global__ __launch_bounds__(kThreads, kWavesPerSimd) void gemm_kernel(const _Fl
     // INT8 (B twice GPTQ's bytes): M first within an XCD's run of tiles, so a
     // few weight strips serve every M tile while they sit in that XCD's L2
     // (configs[2]: 2-3.5% faster; GPTQ: no change).
-    const int mt = I8 ? id % MT : id / NT, nt = I8 ? id / MT : id % NT;
+    const int mt = I8 ? id % MT : id / NT;
+    int nt = I8 ? id / MT : id % NT;
+    if (C1 && nt >= NT1) {  // uniform per workgroup: the second weight's tile
+        nt -= NT1;
+        qw = qw1;
+        sc = sc1;
+        qz = qz1;
+        C = C1;
+    }
     const int m0 = mt * BM, n0 = nt * BN;
     const int nw = n0 + 32 * CB * (wave % WN);  // this wave's columns
     const int mw = 32 * RB * (wave / WN);       // and its rows within the tile
@@ -631,25 +642,32 @@ struct GemmArgs {
     void *C;
     bool f16out;
     int M, K, N;
+    // optional second weight on the same A (C1 != NULL; no split-K)
+    const uint32_t *qw1 = nullptr;
+    const uint16_t *sc1 = nullptr;
+    const uint32_t *qz1 = nullptr;
+    void *C1 = nullptr;
 };
 
 // The staged epilogue needs 16-byte aligned rows: C (or the workspace
 // partials) 16-byte aligned and N a multiple of the elements per 16 bytes.
 int vec_ok(const GemmArgs &g, const Split &sp) {
     if (sp.part) return g.N % 4 == 0;
-    return st::aligned16(g.C) && g.N % (g.f16out ? 8 : 4) == 0;
+    return st::aligned16(g.C) && (!g.C1 || st::aligned16(g.C1)) && g.N % (g.f16out ? 8 : 4) == 0;
 }
 
 template <int GS, bool TILED, int CBL, bool I8>
 int launch_cb(st_context *ctx, const GemmArgs &g, const Split &sp) {
-    const int T = ((g.M + BM - 1) / BM) * ((g.N + 32 * CBL * WN - 1) / (32 * CBL * WN));
+    const int T = ((g.M + BM - 1) / BM) * ((g.N + 32 * CBL * WN - 1) / (32 * CBL * WN)) * (g.C1 ? 2 : 1);
     const dim3 grid(T * sp.S);
     if (g.f16out)
         hipLaunchKernelGGL((gemm_kernel<GS, TILED, true, CBL, I8>), grid, dim3(kThreads), 0, ctx->stream, g.A, g.qw, g.sc,
-                           g.qz, g.zoff, g.rsc, g.chs, g.C, g.M, g.K, g.N, sp.kps, sp.part, vec_ok(g, sp));
+                           g.qz, g.zoff, g.rsc, g.chs, g.C, g.M, g.K, g.N, sp.kps, sp.part, vec_ok(g, sp), g.qw1, g.sc1,
+                           g.qz1, g.C1);
     else
         hipLaunchKernelGGL((gemm_kernel<GS, TILED, false, CBL, I8>), grid, dim3(kThreads), 0, ctx->stream, g.A, g.qw, g.sc,
-                           g.qz, g.zoff, g.rsc, g.chs, g.C, g.M, g.K, g.N, sp.kps, sp.part, vec_ok(g, sp));
+                           g.qz, g.zoff, g.rsc, g.chs, g.C, g.M, g.K, g.N, sp.kps, sp.part, vec_ok(g, sp), g.qw1, g.sc1,
+                           g.qz1, g.C1);
     return st::launch_check("gemm_kernel");
 }
 
@@ -723,12 +741,23 @@ Split plan_split(st_context *ctx, int M, int K, int N, int cb, size_t ws_used) {
 
 namespace {
 
-// The prefill GEMM behind both entry points: u == NULL for a . dequant(W),
-// else silu(a) * u . dequant(W).
+// One weight set of a GEMM call.
+struct GptqOperand {
+    const uint32_t *qweight;
+    const uint16_t *scales;
+    const uint32_t *qzeros;
+    void *c;
+};
+
+// The prefill GEMM behind the entry points: u == NULL for a . dequant(W),
+// else silu(a) * u . dequant(W); with w1 (u == NULL) also C1 = a . dequant(W1)
+// from the same pre-processed A.
 int gemm_impl(const char *fn, st_context *ctx, const uint16_t *a, const uint16_t *u, const uint32_t *qweight,
               const uint16_t *scales, const uint32_t *qzeros, const int32_t *perm, void *c, int c_dtype, int M, int K,
-              int N, int group_size, uint32_t flags) {
+              int N, int group_size, uint32_t flags, const GptqOperand *w1 = nullptr) {
     if (!ctx || !a || !qweight || !scales || !c) return st::fail(ST_ERR_INVALID, "%s: NULL argument", fn);
+    if (w1 && (!w1->qweight || !w1->scales || !w1->c)) return st::fail(ST_ERR_INVALID, "%s: NULL argument", fn);
+    if (w1 && !st::aligned16(w1->qweight)) return st::fail(ST_ERR_ALIGN, "%s: qweight must be 16-byte aligned", fn);
     if (group_size != 64 && group_size != 128 && group_size != 256)
         return st::fail(ST_ERR_SHAPE, "%s: group_size %d not in {64,128,256}", fn, group_size);
     if (M < 1 || K <= 0 || K % KT || K % group_size || N <= 0 || N % 8)
@@ -753,12 +782,36 @@ int gemm_impl(const char *fn, st_context *ctx, const uint16_t *a, const uint16_t
     hipLaunchKernelGGL(prep_a_kernel, dim3(M), dim3(256), (size_t)K * sizeof(_Float16), ctx->stream,
                        reinterpret_cast<const _Float16 *>(a), reinterpret_cast<const _Float16 *>(u), perm, A, rsc, K);
     if (int rc = st::launch_check("prep_a_kernel")) return rc;
-    const GemmArgs g{A, qweight, scales, qzeros, (flags & ST_FLAG_ZEROS_PLUS_ONE) ? 1 : 0, rsc, nullptr, c,
-                     c_dtype == ST_F16, M, K, N};
+    GemmArgs g{A, qweight, scales, qzeros, (flags & ST_FLAG_ZEROS_PLUS_ONE) ? 1 : 0, rsc, nullptr, c,
+               c_dtype == ST_F16, M, K, N};
+    auto run = [&](const GemmArgs &ga, int cb, const Split &sp) {
+        return (flags & ST_FLAG_TILED) ? launch_tiled<true>(ctx, ga, group_size, cb, sp)
+                                       : launch_tiled<false>(ctx, ga, group_size, cb, sp);
+    };
+    if (w1) {
+        // Both weights' tiles in one grid when that needs no split-K (the
+        // partials are laid out for one C); otherwise two launches on A.
+        const int cb2 = pick_cb(ctx, M, 2 * N, false);
+        const Split sp2 = plan_split(ctx, M, K, 2 * N, cb2, need);
+        if (sp2.S == 1) {
+            GemmArgs g2 = g;
+            g2.qw1 = w1->qweight;
+            g2.sc1 = w1->scales;
+            g2.qz1 = w1->qzeros;
+            g2.C1 = w1->c;
+            return run(g2, cb2, sp2);
+        }
+    }
     const int cb = pick_cb(ctx, M, N, false);
     const Split sp = plan_split(ctx, M, K, N, cb, need);
-    if (flags & ST_FLAG_TILED) return launch_tiled<true>(ctx, g, group_size, cb, sp);
-    return launch_tiled<false>(ctx, g, group_size, cb, sp);
+    if (int rc = run(g, cb, sp)) return rc;
+    if (!w1) return ST_OK;
+    GemmArgs g1 = g;
+    g1.qw = w1->qweight;
+    g1.sc = w1->scales;
+    g1.qz = w1->qzeros;
+    g1.C = w1->c;
+    return run(g1, cb, sp);
 }
 
 }  // namespace
@@ -768,6 +821,16 @@ extern "C" int st_gptq_i4_gemm(st_context *ctx, const uint16_t *a, const uint32_
                                int group_size, uint32_t flags) {
     return gemm_impl("st_gptq_i4_gemm", ctx, a, nullptr, qweight, scales, qzeros, perm, c, c_dtype, M, K, N, group_size,
                      flags);
+}
+
+extern "C" int st_gptq_i4_gate_up_gemm(st_context *ctx, const uint16_t *a, const uint32_t *gate_qweight,
+                                       const uint16_t *gate_scales, const uint32_t *gate_qzeros,
+                                       const uint32_t *up_qweight, const uint16_t *up_scales, const uint32_t *up_qzeros,
+                                       const int32_t *perm, void *c_gate, void *c_up, int c_dtype, int M, int K, int N,
+                                       int group_size, uint32_t flags) {
+    const GptqOperand up{up_qweight, up_scales, up_qzeros, c_up};
+    return gemm_impl("st_gptq_i4_gate_up_gemm", ctx, a, nullptr, gate_qweight, gate_scales, gate_qzeros, perm, c_gate,
+                     c_dtype, M, K, N, group_size, flags, &up);
 }
 
 extern "C" int st_gptq_i4_silu_gemm(st_context *ctx, const uint16_t *gate, const uint16_t *up, const uint32_t *qweight,

@@ -45,6 +45,8 @@ class DecoderLinears:
             raise ValueError("inconsistent layer shapes")
         if (gate.perm is None) != (up.perm is None) or (gate.perm is not None and not bool((gate.perm == up.perm).all())):
             raise ValueError("gate and up must share their act-order permutation (one fused call)")
+        if gate.flags != up.flags or gate.group_size != up.group_size:
+            raise ValueError("gate and up must share their layout flags and group size (one fused call)")
         self.qkv = GptqWeight.cat([q, k, v])
         self.splits = (q.N, k.N, v.N)
         self.o, self.gate, self.up, self.down = o, gate, up, down
@@ -92,8 +94,11 @@ class DecoderLinears:
         """x [M, hidden] and attn [M, attn_dim] f16. Writes qkv_out, o_out,
         gate_out [M, inter], up_out [M, inter] and down_out [M, hidden] =
         (silu(gate) * up).Wd, all f16 (each feeds the next GEMM)."""
-        for w, a, c in ((self.qkv, x, qkv_out), (self.o, attn, o_out), (self.gate, x, gate_out), (self.up, x, up_out)):
+        for w, a, c in ((self.qkv, x, qkv_out), (self.o, attn, o_out)):
             M.gptq_gemm(gpu, a, w.qweight, w.scales, c, w.K, w.N, w.group_size, w.qzeros, w.perm, w.flags)
+        g, u = self.gate, self.up
+        M.gate_up_gemm(gpu, x, g.qweight, g.scales, u.qweight, u.scales, gate_out, up_out, g.K, g.N, g.group_size,
+                       g.qzeros, u.qzeros, g.perm, g.flags)
         d = self.down
         M.fused_silu_gptq_gemm(gpu, gate_out, up_out, d.qweight, d.scales, down_out, d.K, d.N, d.group_size,
                                d.qzeros, d.perm, d.flags)

@@ -166,6 +166,24 @@ def gptq_gemm(gpu, a, qweight, scales, c, k: int, n: int, group_size: int = 128,
          k, n, group_size, flags)
 
 
+def gate_up_gemm(gpu, a, gate_qw, gate_sc, up_qw, up_sc, gate_out, up_out, k: int, n: int, group_size: int = 128,
+                 gate_qz=None, up_qz=None, perm=None, flags: int = 0) -> None:
+    """gate_out = a . dequant(Wg) and up_out = a . dequant(Wu), [M, n] each,
+    float32 or float16 (one dtype), from one pass over a (f16): the M-token
+    gate and up projections of src/model.rs:803-811, each bit for bit what
+    gptq_gemm gives for that weight."""
+    import torch
+
+    _check_gptq(gate_qw, gate_sc, gate_qz, perm, k, n, group_size, flags)
+    _check_gptq(up_qw, up_sc, up_qz, perm, k, n, group_size, flags)
+    m = _check_io(a, k, gate_out, n, x_dtypes=(torch.float16,), out_dtypes=(torch.float32, torch.float16), name="a")
+    _need(up_out, "up_out", (gate_out.dtype,), m * n)
+    cd = ST_F32 if gate_out.dtype == torch.float32 else ST_F16
+    gpu.sync_stream()
+    call("st_gptq_i4_gate_up_gemm", gpu.handle, ptr(a), ptr(gate_qw), ptr(gate_sc), ptr(gate_qz), ptr(up_qw),
+         ptr(up_sc), ptr(up_qz), ptr(perm), ptr(gate_out), ptr(up_out), cd, m, k, n, group_size, flags)
+
+
 def fused_silu_gptq_gemm(gpu, gate_out, up_out, down_qw, down_sc, output, k: int, n: int, group_size: int = 128,
                          qzeros=None, perm=None, flags: int = 0) -> None:
     """output[M, n] = (silu(gate_out) * up_out)[M, k] . dequant(W): the

@@ -234,3 +234,74 @@ def test_gemm_unaligned_c_matches_aligned(gpu, orc, out_dtype):
     assert torch.equal(aligned, shifted)
     ref = orc.gptq_matvec_f64(c["x"], c["qweight"], c["scales"], K, N, gs, qzeros=c["qzeros"])
     assert orc.rel_l2(aligned.float().cpu().numpy(), ref) < 5e-4
+
+
+def run_gate_up(gpu, wg, wu, a_np, out_dtype=torch.float32):
+    a = torch.from_numpy(np.ascontiguousarray(a_np, dtype=np.float16)).to(gpu.device)
+    cg = torch.full((a.shape[0], wg.N), float("nan"), dtype=out_dtype, device=gpu.device)
+    cu = torch.full_like(cg, float("nan"))
+    M.gate_up_gemm(gpu, a, wg.qweight, wg.scales, wu.qweight, wu.scales, cg, cu, wg.K, wg.N, wg.group_size,
+                   wg.qzeros, wu.qzeros, wg.perm, wg.flags)
+    torch.cuda.synchronize()
+    return cg.float().cpu().numpy(), cu.float().cpu().numpy()
+
+
+@pytest.mark.parametrize("Mr,K,N,gs,zeros,act,tiled,out", [
+    (512, 2560, 9728, 128, False, False, True, torch.float16),  # configs[4] gate/up at a 512-token prefill: one grid
+    (300, 1536, 776, 64, True, True, False, torch.float32),     # act-order, zeros, row-major qweight
+    (257, 2048, 520, 256, True, False, True, torch.float16),    # group 256, ragged M
+    (64, 4096, 264, 128, False, False, True, torch.float32),    # few tiles: split-K, two launches on one A
+    (33, 1024, 1032, 128, "up", False, True, torch.float32),    # zero points on up only
+])
+def test_gate_up_gemm_equals_two_gemms(gpu, orc, Mr, K, N, gs, zeros, act, tiled, out):
+    """st_gptq_i4_gate_up_gemm: each output bit for bit what st_gptq_i4_gemm
+    gives for that weight (one grid over both weights' tiles, or two
+    launches on the shared pre-processed A when K is split), and within the
+    GEMM bar of the f64 oracle."""
+    cg = orc.gptq_case(600 + Mr, K, N, gs, zeros=zeros is True, act_order=act, M=Mr, x_dtype=np.float16)
+    cu = orc.gptq_case(700 + Mr, K, N, gs, zeros=bool(zeros), act_order=act)
+    cu["g_idx"] = cg["g_idx"]
+    wg, wu = up(gpu, cg, tiled=tiled), up(gpu, cu, tiled=tiled)
+    assert (wg.qzeros is None) == (zeros is not True) and (wu.qzeros is None) == (not zeros)
+    yg, yu = run_gate_up(gpu, wg, wu, cg["x"], out)
+    np.testing.assert_array_equal(yg, run_gemm(gpu, wg, cg["x"], out))
+    np.testing.assert_array_equal(yu, run_gemm(gpu, wu, cg["x"], out))
+    for cc, y in ((cg, yg), (cu, yu)):
+        ref = orc.gptq_matvec_f64(cg["x"], cc["qweight"], cc["scales"], K, N, gs, qzeros=cc["qzeros"],
+                                  g_idx=cg["g_idx"])
+        e = orc.rel_l2(y, ref)
+        print(f"gate/up gemm M={Mr} K={K} N={N} gs={gs} zeros={zeros} act={act}: rel-L2 {e:.3e}")
+        assert e < TOL
+
+
+def test_gate_up_gemm_graph_replay(gpu, orc):
+    """Captured once, replayed three times with eager work between: both
+    outputs equal the eager call's bit for bit every time."""
+    Mr, K, N, gs = 256, 1024, 2048, 128
+    cg = orc.gptq_case(80, K, N, gs, zeros=True, M=Mr, x_dtype=np.float16)
+    cu = orc.gptq_case(81, K, N, gs, zeros=True)
+    wg, wu = up(gpu, cg), up(gpu, cu)
+    a = torch.from_numpy(cg["x"].astype(np.float16)).to(gpu.device)
+    eg, eu = (torch.empty(Mr, N, device=gpu.device) for _ in range(2))
+    call = lambda g_, u_: M.gate_up_gemm(gpu, a, wg.qweight, wg.scales, wu.qweight, wu.scales, g_, u_, K, N, gs,
+                                         wg.qzeros, wu.qzeros, None, wg.flags)
+    call(eg, eu)
+    torch.cuda.synchronize()
+    og, ou = torch.empty_like(eg), torch.empty_like(eu)
+    s = torch.cuda.Stream()
+    with torch.cuda.stream(s):
+        call(og, ou)
+        torch.cuda.synchronize()
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph, stream=s):
+            call(og, ou)
+    for i in range(3):
+        og.fill_(float("nan"))
+        ou.fill_(float("nan"))
+        torch.cuda.synchronize()
+        with torch.cuda.stream(s):
+            graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(og, eg) and torch.equal(ou, eu), f"replay {i}"
+        call(eg, eu)  # eager work between
+        torch.cuda.synchronize()
