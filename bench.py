@@ -364,10 +364,21 @@ def main():
                      "frac": round(gu_gbs / HBM_PEAK_GBS, 4), "traffic": load_traffic()},
     }
 
+    sc = bench_stream_ceiling(torch, dev, args, {"q_proj": b_q, "gate_up": b_gu, "down": b_dn,
+                                                  "lm_head_int4": decode_bytes(2560, 151936, 4, 151936)})
+    out["stream_ceiling"] = sc
+    if "gate_up" in sc:
+        for k in ("q_proj", "gate_up", "down"):
+            out["kernels"][k]["frac_of_stream"] = round(sc[k]["ms"] / out["kernels"][k]["ms"], 4)
+        out["roofline"]["stream_ceiling_GB/s"] = sc["gate_up"]["GB/s"]
+        out["roofline"]["frac_of_stream"] = out["kernels"]["gate_up"]["frac_of_stream"]
+
     if not args.no_gemm:
         out["gemm"] = bench_gemm(torch, dev, gpu, Mdl, gen, args)
     out["lm_head_bf16"] = bench_lm_head(torch, dev, gpu, Mdl, gen, args)
     out["lm_head_int4"] = bench_lm_head_int4(torch, dev, gpu, Mdl, gen, args)
+    if "lm_head_int4" in sc:
+        out["lm_head_int4"]["M1"]["frac_of_stream"] = round(sc["lm_head_int4"]["ms"] / out["lm_head_int4"]["M1"]["ms"], 4)
     out["int8_cfg2"] = bench_int8(torch, dev, gpu, Mdl, gen, args)
     if not args.no_stack:
         out["stack_cfg4"] = bench_stack(torch, dev, gpu, Mdl, gen, args)
@@ -376,6 +387,48 @@ def main():
         out["cpu_baseline"] = cpu_baseline(args.cpu_seconds)
     gpu.close()
     print(json.dumps(out))
+
+
+def bench_stream_ceiling(torch, dev, args, sizes):
+    """The plain-stream ceiling of each decode launch: a kernel that only
+    reads the same number of bytes (libshady_probe.so, 16-byte nontemporal
+    loads, eight in flight per lane, no compute), timed like the kernels
+    (graph replay, each call on its own window of a 1 GiB buffer, so every
+    read comes from HBM), best over four grid sizes. What a launch of that
+    size can reach on this box; the kernels' `frac_of_stream` is measured
+    against it."""
+    import ctypes
+
+    path = os.path.join(ROOT, "shady_thinker_amd", "libshady_probe.so")
+    if not os.path.exists(path):
+        return {"status": "libshady_probe.so not built"}
+    lib = ctypes.CDLL(path)
+    lib.stp_read.restype = ctypes.c_int
+    lib.stp_read.argtypes = [ctypes.c_void_p, ctypes.c_size_t, ctypes.c_void_p, ctypes.c_int, ctypes.c_int, ctypes.c_int,
+                            ctypes.c_void_p]
+    total = 1 << 30
+    buf = torch.randint(-(2**31), 2**31 - 1, (total // 4,), dtype=torch.int32, device=dev)
+    sink = torch.zeros(4096, dtype=torch.int32, device=dev)
+    out = {"probe": "stream_read_kernel (libshady_probe.so): read-only, 16-byte nontemporal loads, 256 threads "
+                    "per workgroup, best of grids 256/512/1024/2048; graph replay, cold windows of a 1 GiB buffer"}
+    for name, nbytes in sizes.items():
+        nb = (nbytes + 255) // 256 * 256
+        period = max(2, min(64, total // nb))
+        best = None
+        for grid in (256, 512, 1024, 2048):
+            def rd(i, grid=grid):
+                r = lib.stp_read(buf.data_ptr() + (i % period) * nb, nb, sink.data_ptr(), grid, 256, 0,
+                                 torch.cuda.current_stream().cuda_stream)
+                if r:
+                    raise RuntimeError(f"stp_read -> {r}")
+            ms = Replayer(torch, rd, period).run(max(20, args.steps // 2), 5)
+            if best is None or ms < best[0]:
+                best = (ms, grid)
+        gbs = nb / (best[0] * 1e-3) / 1e9
+        out[name] = {"bytes": nb, "ms": round(best[0], 5), "GB/s": round(gbs, 1),
+                     "hbm_frac": round(gbs / HBM_PEAK_GBS, 4), "grid": best[1]}
+    del buf
+    return out
 
 
 def bench_gemm(torch, dev, gpu, Mdl, gen, args):

@@ -1,0 +1,78 @@
+// Plain streaming read, the measuring stick for the decode kernels: a kernel
+// that reads `bytes` of device memory once (16-byte nontemporal loads, eight
+// in flight per lane) and does nothing else. bench.py times it on buffers of
+// each decode kernel's algorithmic byte count, with the same graph replay and
+// cold-cache rotation as the kernels, so each kernel's time can be set beside
+// the fastest a launch of that size can read its bytes on the same box.
+// Not part of the product path (a separate library, libshady_probe.so, loaded
+// only by the benchmark); it has no reference counterpart.
+#include <hip/hip_runtime.h>
+
+#include <cstddef>
+#include <cstdint>
+
+namespace {
+
+typedef unsigned u32x4 __attribute__((ext_vector_type(4)));
+
+constexpr int kUnroll = 8;
+
+// MODE 0: grid-strided (consecutive 16-byte chunks go to consecutive lanes
+// of the whole grid). MODE 1: workgroup b reads its own contiguous range
+// (the decode kernels' split of tiles over CUs). MODE 2: every wave reads
+// its own contiguous range (the streaming decode kernel's split over waves).
+template <int MODE>
+__global__ __launch_bounds__(1024) void stream_read_kernel(const u32x4 *__restrict__ p, size_t n16,
+                                                           unsigned *__restrict__ sink) {
+    size_t i, end, stride;
+    if constexpr (MODE == 0) {
+        stride = (size_t)gridDim.x * blockDim.x;
+        i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+        end = n16;
+    } else {
+        const size_t parts = MODE == 1 ? gridDim.x : (size_t)gridDim.x * (blockDim.x / 64);
+        const size_t part = MODE == 1 ? blockIdx.x : (size_t)blockIdx.x * (blockDim.x / 64) + threadIdx.x / 64;
+        const size_t lanes = MODE == 1 ? blockDim.x : 64;
+        const size_t lane = MODE == 1 ? threadIdx.x : threadIdx.x % 64;
+        const size_t per = (n16 + parts - 1) / parts;
+        const size_t b = part * per;
+        end = b + per < n16 ? b + per : n16;
+        i = b + lane;
+        stride = lanes;
+    }
+    unsigned acc = 0;
+    // Full rounds: kUnroll independent loads issued before any is used.
+    for (; i + (kUnroll - 1) * stride < end; i += kUnroll * stride) {
+        u32x4 v[kUnroll];
+#pragma unroll
+        for (int u = 0; u < kUnroll; ++u) v[u] = __builtin_nontemporal_load(p + i + u * stride);
+#pragma unroll
+        for (int u = 0; u < kUnroll; ++u) acc ^= v[u].x ^ v[u].y ^ v[u].z ^ v[u].w;
+    }
+    for (; i < end; i += stride) {
+        const u32x4 v = __builtin_nontemporal_load(p + i);
+        acc ^= v.x ^ v.y ^ v.z ^ v.w;
+    }
+    // Data-dependent store that never happens for the benchmark's buffers
+    // (keeps the loads alive without writing anything).
+    if (acc == 0x9E3779B9u) sink[blockIdx.x] = acc;
+}
+
+}  // namespace
+
+// grid workgroups of `block` threads (64..1024, a multiple of 64); sink holds
+// at least `grid` words.
+extern "C" int stp_read(const void *buf, size_t bytes, unsigned *sink, int grid, int block, int mode, void *stream) {
+    if (!buf || !sink || grid <= 0 || block < 64 || block > 1024 || block % 64 || bytes % 16 || (uintptr_t)buf % 16 ||
+        mode < 0 || mode > 2)
+        return 1;
+    const u32x4 *p = reinterpret_cast<const u32x4 *>(buf);
+    const hipStream_t s = (hipStream_t)stream;
+    if (mode == 0)
+        hipLaunchKernelGGL(stream_read_kernel<0>, dim3(grid), dim3(block), 0, s, p, bytes / 16, sink);
+    else if (mode == 1)
+        hipLaunchKernelGGL(stream_read_kernel<1>, dim3(grid), dim3(block), 0, s, p, bytes / 16, sink);
+    else
+        hipLaunchKernelGGL(stream_read_kernel<2>, dim3(grid), dim3(block), 0, s, p, bytes / 16, sink);
+    return hipGetLastError() == hipSuccess ? 0 : 2;
+}
