@@ -280,6 +280,12 @@ __global__ __launch_bounds__(kThreads) void i4mm_kernel(const void *__restrict__
 #pragma unroll
         for (int i = 0; i < YV; ++i) ys[mb][i] = 0.f;
 
+    // A wave without a tile (its workgroup owns fewer tiles than it has wave
+    // groups) computes on: its sums are never used, a branch around the work
+    // made the compiler's load waits drain everything in flight, and with its
+    // x reads all on one address (a broadcast) they take one LDS access
+    // instead of eight from the other waves.
+    const int amask = active ? -1 : 0;
     auto compute = [&](const _Float16 *xs, const float *ps, const Unit<GS> (&src_u)[GW]) {
 #pragma unroll
         for (int gi = 0; gi < GW; ++gi) {
@@ -307,7 +313,7 @@ __global__ __launch_bounds__(kThreads) void i4mm_kernel(const void *__restrict__
                     const int kk = ul * 128 + 64 * st + 16 * q + 8 * h;
 #pragma unroll
                     for (int mb = 0; mb < MB; ++mb) {
-                        const half8 a = *reinterpret_cast<const half8 *>(&xs[(16 * mb + r16) * kPitch + kk]);
+                        const half8 a = *reinterpret_cast<const half8 *>(&xs[((16 * mb + r16) * kPitch + kk) & amask]);
                         acc[mb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, acc[mb], 0, 0, 0);
                     }
                 }

@@ -144,13 +144,13 @@ __global__ __launch_bounds__(kThreads) void i8mm_kernel(const _Float16 *__restri
     for (int c = 0; c < nch; c += 2) {
         load_x(c + 1);
         load_w(wr[1], c + 1);
-        compute(xs0, wr[0]);
+        if (active) compute(xs0, wr[0]);  // a wave without a tile skips the work (and its LDS reads)
         store_x(xs1);
         lds_barrier();
         if (c + 1 >= nch) break;
         load_x(c + 2);
         load_w(wr[0], c + 2);
-        compute(xs1, wr[1]);
+        if (active) compute(xs1, wr[1]);
         store_x(xs0);
         lds_barrier();
     }
