@@ -114,6 +114,7 @@ typedef enum {
     ST_TUNE_STREAM_TILES_WG,   /* streaming decode kernel: 16-column tiles per workgroup (0: a workgroup per CU) */
     ST_TUNE_STREAM_SYNC,       /* streaming decode kernel: ring blocks between workgroup barriers (0: none) */
     ST_TUNE_SPLIT_REDUCE_KERNEL, /* several-token split-K decode: 1 reduce kernel, 0 fused (default: fused up to 8 tokens) */
+    ST_TUNE_I4MM_WAVES,        /* f16-MFMA GPTQ decode: 16 forces 16-wave workgroups (default: 12 when the tiles use at most 12) */
     ST_TUNE_COUNT
 } st_tune;
 int st_context_set_tune(st_context *ctx, int knob, int value);

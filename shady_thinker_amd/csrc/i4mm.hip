@@ -152,8 +152,10 @@ __global__ __launch_bounds__(256) void i4mm_prep_kernel(const float *__restrict_
 // NSRC: 1 (matvec) or 2 (gate/up); MB: 16-row MFMA blocks; KCU: 128-k units
 // per staged chunk; GW: units per wave per chunk (S = KCU / GW waves per tile
 // and source).
-template <bool F32X, int NSRC, int MB, int GS, int KCU, int GW>
-__global__ __launch_bounds__(kThreads) void i4mm_kernel(const void *__restrict__ x, const float *__restrict__ pe,
+// NW waves per workgroup: 16, or 12 when the workgroup's tiles use at most 12
+// (a wave without a tile still issues every VALU instruction of the loop).
+template <bool F32X, int NSRC, int MB, int GS, int KCU, int GW, int NW>
+__global__ __launch_bounds__(64 * NW) void i4mm_kernel(const void *__restrict__ x, const float *__restrict__ pe,
                                                         const uint32_t *__restrict__ qw0,
                                                         const uint16_t *__restrict__ sc0, const uint32_t *__restrict__ qz0,
                                                         const uint32_t *__restrict__ qw1, const uint16_t *__restrict__ sc1,
@@ -170,9 +172,10 @@ __global__ __launch_bounds__(kThreads) void i4mm_kernel(const void *__restrict__
     // x items of 8 k: rows (tokens, or hi/lo rows of f32 tokens) x kKC / 8
     // per chunk, one 16-byte load each
     constexpr int XITEMS = ROWS * (kKC / 8);
-    constexpr int XL = (XITEMS + kThreads - 1) / kThreads;
+    constexpr int kThr = 64 * NW;
+    constexpr int XL = (XITEMS + kThr - 1) / kThr;
     // two x buffers; at the end, the partial sums of every wave
-    constexpr int kRedBytes = kWaves * MB * (F32X ? 2 : 4) * 64 * 4;
+    constexpr int kRedBytes = NW * MB * (F32X ? 2 : 4) * 64 * 4;
     constexpr int kXsHalves = 2 * ROWS * kPitch > kRedBytes / 2 ? 2 * ROWS * kPitch : kRedBytes / 2;
     __shared__ __align__(16) _Float16 xs[kXsHalves];
     _Float16 *const xs0 = xs, *const xs1 = xs + ROWS * kPitch;
@@ -217,7 +220,7 @@ __global__ __launch_bounds__(kThreads) void i4mm_kernel(const void *__restrict__
     auto load_x = [&](u32x4 (&xr)[XL], unsigned &pr, int c) {
 #pragma unroll
         for (int j = 0; j < XL; ++j) {
-            const int i = j * kThreads + tid;
+            const int i = j * kThr + tid;
             const int row = i / (kKC / 8), k = c * kKC + 8 * (i % (kKC / 8));
             const bool ok = i < XITEMS && row < nrows && k < K;
             xr[j] = __builtin_amdgcn_raw_buffer_load_b128(rx, ok ? (unsigned)(row * K + k) * 2u : kNoLoad, 0, 0);
@@ -231,8 +234,8 @@ __global__ __launch_bounds__(kThreads) void i4mm_kernel(const void *__restrict__
     auto store_x = [&](const u32x4 (&xr)[XL], unsigned pr, _Float16 *xs, float *ps) {
 #pragma unroll
         for (int j = 0; j < XL; ++j) {
-            const int i = j * kThreads + tid;
-            if (XITEMS % kThreads == 0 || i < XITEMS)
+            const int i = j * kThr + tid;
+            if (XITEMS % kThr == 0 || i < XITEMS)
                 *reinterpret_cast<u32x4 *>(&xs[(i / (kKC / 8)) * kPitch + 8 * (i % (kKC / 8))]) =
                     F32X ? xr[j] : to_b_order(xr[j]);
         }
@@ -365,7 +368,7 @@ __global__ __launch_bounds__(kThreads) void i4mm_kernel(const void *__restrict__
 
     // Partial sums of the S waves of a tile (and source), added in slice order.
     float *red = reinterpret_cast<float *>(xs);
-    static_assert(kWaves * MB * YV * 64 * 4 == kRedBytes, "reduction buffer");
+    static_assert(NW * MB * YV * 64 * 4 == kRedBytes, "reduction buffer");
 #pragma unroll
     for (int mb = 0; mb < MB; ++mb)
 #pragma unroll
@@ -392,25 +395,32 @@ __global__ __launch_bounds__(kThreads) void i4mm_kernel(const void *__restrict__
 
 template <bool F32X, int NSRC, int MB, int GS>
 int launch_gs(st_context *ctx, const void *x, const float *pe, const uint32_t *const *qw, const uint16_t *const *sc,
-              const uint32_t *const *qz, int zoff, float *y, int M, int K, int N, int ntiles, int G, int wpt) {
-    const dim3 grid(G), block(kThreads);
-#define ST_I4MM(KCU_, GW_)                                                                                      \
-    hipLaunchKernelGGL((i4mm_kernel<F32X, NSRC, MB, GS, KCU_, GW_>), grid, block, 0, ctx->stream, x, pe, qw[0], sc[0], \
-                       qz[0], qw[1], sc[1], qz[1], zoff, y, M, K, N, ntiles)
+              const uint32_t *const *qz, int zoff, float *y, int M, int K, int N, int ntiles, int G, int wpt, int nw) {
+    const dim3 grid(G);
+#define ST_I4MM(KCU_, GW_, NW_)                                                                                  \
+    hipLaunchKernelGGL((i4mm_kernel<F32X, NSRC, MB, GS, KCU_, GW_, NW_>), grid, dim3(64 * NW_), 0, ctx->stream, x, pe, \
+                       qw[0], sc[0], qz[0], qw[1], sc[1], qz[1], zoff, y, M, K, N, ntiles)
     // waves per tile and source = 128-k units per chunk (one unit per wave):
     // 8 (1024-k chunks), 4 or 2. Group size 64 stops at 4: its 8-unit chunk
     // spilled 30 VGPRs inside the loop (one source, 16 tokens, 2560 x 6144:
     // 15.5 -> 13.7 us with 4; gate/up unchanged).
     if constexpr (GS != 64) {
         if (wpt >= 8) {
-            ST_I4MM(8, 1);
+            ST_I4MM(8, 1, 16);
             return st::launch_check("i4mm_kernel");
         }
     }
-    if (wpt >= 4)
-        ST_I4MM(4, 1);
-    else
-        ST_I4MM(2, 1);
+    if (wpt >= 4) {
+        if (nw == 12)
+            ST_I4MM(4, 1, 12);
+        else
+            ST_I4MM(4, 1, 16);
+    } else {
+        if (nw == 12)
+            ST_I4MM(2, 1, 12);
+        else
+            ST_I4MM(2, 1, 16);
+    }
 #undef ST_I4MM
     return st::launch_check("i4mm_kernel");
 }
@@ -431,21 +441,23 @@ __global__ __launch_bounds__(256) void i4mm_gather_kernel(const uint16_t *__rest
 
 template <bool F32X, int NSRC, int MB>
 int launch_mb(st_context *ctx, const void *x, const float *pe, const uint32_t *const *qw, const uint16_t *const *sc,
-              const uint32_t *const *qz, int zoff, float *y, int M, int K, int N, int gs, int ntiles, int G, int wpt) {
+              const uint32_t *const *qz, int zoff, float *y, int M, int K, int N, int gs, int ntiles, int G, int wpt,
+              int nw) {
     switch (gs) {
-        case 64: return launch_gs<F32X, NSRC, MB, 64>(ctx, x, pe, qw, sc, qz, zoff, y, M, K, N, ntiles, G, wpt);
-        case 128: return launch_gs<F32X, NSRC, MB, 128>(ctx, x, pe, qw, sc, qz, zoff, y, M, K, N, ntiles, G, wpt);
-        default: return launch_gs<F32X, NSRC, MB, 256>(ctx, x, pe, qw, sc, qz, zoff, y, M, K, N, ntiles, G, wpt);
+        case 64: return launch_gs<F32X, NSRC, MB, 64>(ctx, x, pe, qw, sc, qz, zoff, y, M, K, N, ntiles, G, wpt, nw);
+        case 128: return launch_gs<F32X, NSRC, MB, 128>(ctx, x, pe, qw, sc, qz, zoff, y, M, K, N, ntiles, G, wpt, nw);
+        default: return launch_gs<F32X, NSRC, MB, 256>(ctx, x, pe, qw, sc, qz, zoff, y, M, K, N, ntiles, G, wpt, nw);
     }
 }
 
 template <bool F32X, int NSRC>
 int launch_src(st_context *ctx, const void *x, const float *pe, const uint32_t *const *qw, const uint16_t *const *sc,
-               const uint32_t *const *qz, int zoff, float *y, int M, int K, int N, int gs, int ntiles, int G, int wpt) {
+               const uint32_t *const *qz, int zoff, float *y, int M, int K, int N, int gs, int ntiles, int G, int wpt,
+               int nw) {
     // tokens per 16-row block: 8 (f32 x: hi and lo rows) or 16
     const int mb = (M * (F32X ? 2 : 1) + 15) / 16;
-    return mb <= 1 ? launch_mb<F32X, NSRC, 1>(ctx, x, pe, qw, sc, qz, zoff, y, M, K, N, gs, ntiles, G, wpt)
-                   : launch_mb<F32X, NSRC, 2>(ctx, x, pe, qw, sc, qz, zoff, y, M, K, N, gs, ntiles, G, wpt);
+    return mb <= 1 ? launch_mb<F32X, NSRC, 1>(ctx, x, pe, qw, sc, qz, zoff, y, M, K, N, gs, ntiles, G, wpt, nw)
+                   : launch_mb<F32X, NSRC, 2>(ctx, x, pe, qw, sc, qz, zoff, y, M, K, N, gs, ntiles, G, wpt, nw);
 }
 
 }  // namespace
@@ -466,6 +478,9 @@ int int4_mm_f16(st_context *ctx, const void *x, bool x_f32, const int32_t *perm,
     int wpt = 2;  // waves per tile and source: a power of two, wpt * nsrc * tbmax <= 16
     while (wpt < 8 && 2 * wpt * nsrc * tbmax <= kWaves) wpt *= 2;
     if (wpt * nsrc * tbmax > kWaves) return fail(ST_ERR_SHAPE, "int4_mm_f16: %d tiles per workgroup", tbmax);
+    // 12-wave workgroups when the tiles use at most 12 waves (gate/up with 3
+    // tile pairs per workgroup): idle waves would still issue the loop's VALU
+    const int nw = (wpt <= 4 && wpt * nsrc * tbmax <= 12 && tune(ctx, ST_TUNE_I4MM_WAVES, 0) != 16) ? 12 : 16;
     const void *xa = x;
     const float *pe = nullptr;
     if (x_f32) {  // the pre-pass writes [2M, K] f16 rows and [M, K / 128] factors into the workspace
@@ -489,10 +504,10 @@ int int4_mm_f16(st_context *ctx, const void *x, bool x_f32, const int32_t *perm,
         xa = xg;
     }
     if (nsrc == 2)
-        return x_f32 ? launch_src<true, 2>(ctx, xa, pe, qw, sc, qz, zoff, y, M, K, N, gs, ntiles, G, wpt)
-                     : launch_src<false, 2>(ctx, xa, pe, qw, sc, qz, zoff, y, M, K, N, gs, ntiles, G, wpt);
-    return x_f32 ? launch_src<true, 1>(ctx, xa, pe, qw, sc, qz, zoff, y, M, K, N, gs, ntiles, G, wpt)
-                 : launch_src<false, 1>(ctx, xa, pe, qw, sc, qz, zoff, y, M, K, N, gs, ntiles, G, wpt);
+        return x_f32 ? launch_src<true, 2>(ctx, xa, pe, qw, sc, qz, zoff, y, M, K, N, gs, ntiles, G, wpt, nw)
+                     : launch_src<false, 2>(ctx, xa, pe, qw, sc, qz, zoff, y, M, K, N, gs, ntiles, G, wpt, nw);
+    return x_f32 ? launch_src<true, 1>(ctx, xa, pe, qw, sc, qz, zoff, y, M, K, N, gs, ntiles, G, wpt, nw)
+                 : launch_src<false, 1>(ctx, xa, pe, qw, sc, qz, zoff, y, M, K, N, gs, ntiles, G, wpt, nw);
 }
 
 }  // namespace st

@@ -863,6 +863,40 @@ def test_int4_mm_f16(gpu, orc, Mr, K, N, gs, zeros, f16, dual, tune):
 
 
 @pytest.mark.parametrize("Mr,K,N,gs,zeros,f16,dual", [
+    (16, 2560, 9728, 128, False, False, True),   # configs[4] gate/up: 608 tile pairs, 3 per workgroup
+    (9, 1024, 11008, 128, True, True, True),     # Llama-7B gate/up width, f16 x, zeros
+    (12, 1024, 12288, 128, False, False, False),  # one source, 768 tiles: 3 per workgroup, 4 waves each
+    (16, 1024, 20480, 64, True, False, False),   # one source, 1280 tiles: 5 per workgroup, group 64
+])
+def test_int4_mm_f16_12_waves(gpu, orc, Mr, K, N, gs, zeros, f16, dual, tune):
+    """Workgroups whose tiles use at most 12 waves launch 12 (the idle waves
+    of a 16-wave workgroup would still issue the loop's VALU work): same
+    per-wave work and reduction order, so the result equals the 16-wave
+    launch bit for bit, and the f64 oracle within 1e-5."""
+    _force_i4mm(tune)
+    xd = np.float16 if f16 else np.float32
+    c = orc.gptq_case(190 + Mr, K, N, gs, zeros=zeros, M=Mr, x_dtype=xd)
+    w = up(gpu, c)
+    dt = torch.float16 if f16 else torch.float32
+    ref = orc.gptq_matvec_f64(c["x"], c["qweight"], c["scales"], K, N, gs, qzeros=c["qzeros"])
+    if dual:
+        c2 = orc.gptq_case(290 + Mr, K, N, gs, zeros=zeros)
+        w2 = up(gpu, c2)
+        ref = orc.silu_gate_f64(ref, orc.gptq_matvec_f64(c["x"], c2["qweight"], c2["scales"], K, N, gs,
+                                                         qzeros=c2["qzeros"]))
+        run = lambda: _gate_up(gpu, w, w2, c["x"], dt)
+    else:
+        run = lambda: run_matvec(gpu, w, c["x"], dt)
+    y12 = run()
+    tune(I4MM_WAVES=16)
+    y16 = run()
+    e = orc.rel_l2(y12, ref)
+    print(f"int4 f16-MFMA 12 waves M={Mr} K={K} N={N} gs={gs} dual={dual} rel-L2 {e:.3e}")
+    assert np.isfinite(y12).all() and e < 1e-5
+    assert np.array_equal(y12, y16)
+
+
+@pytest.mark.parametrize("Mr,K,N,gs,zeros,f16,dual", [
     (16, 2560, 6144, 128, False, False, False),  # configs[4] q|k|v shape, f32 x (gathered in the pre-pass)
     (12, 1024, 4112, 64, True, True, False),     # f16 x (gather pass), zeros, group 64, 257 tiles
     (16, 2560, 9728, 128, True, False, True),    # gate/up, f32 x
