@@ -413,7 +413,9 @@ def bench_stream_ceiling(torch, dev, args, sizes):
                     "per workgroup, best of grids 256/512/1024/2048; graph replay, cold windows of a 1 GiB buffer"}
     for name, nbytes in sizes.items():
         nb = (nbytes + 255) // 256 * 256
-        period = max(2, min(64, total // nb))
+        if 2 * nb > total:
+            raise ValueError(f"stream ceiling: {nb} bytes needs a buffer above {total} bytes for two cold windows")
+        period = min(64, total // nb)
         best = None
         for grid in (256, 512, 1024, 2048):
             def rd(i, grid=grid):
