@@ -154,7 +154,10 @@ __global__ __launch_bounds__(256) void i4mm_prep_kernel(const float *__restrict_
 // and source).
 // NW waves per workgroup: 16, or 12 when the workgroup's tiles use at most 12
 // (a wave without a tile still issues every VALU instruction of the loop).
-template <bool F32X, int NSRC, int MB, int GS, int KCU, int GW, int NW>
+// PAIR (two sources): a wave takes its units of both the gate and the up
+// weight of a tile, so every x fragment read from LDS and every load
+// address serves two MFMA chains.
+template <bool F32X, int NSRC, int MB, int GS, int KCU, int GW, int NW, bool PAIR>
 __global__ __launch_bounds__(64 * NW) void i4mm_kernel(const void *__restrict__ x, const float *__restrict__ pe,
                                                         const uint32_t *__restrict__ qw0,
                                                         const uint16_t *__restrict__ sc0, const uint32_t *__restrict__ qz0,
@@ -175,7 +178,9 @@ __global__ __launch_bounds__(64 * NW) void i4mm_kernel(const void *__restrict__ 
     constexpr int kThr = 64 * NW;
     constexpr int XL = (XITEMS + kThr - 1) / kThr;
     // two x buffers; at the end, the partial sums of every wave
-    constexpr int kRedBytes = NW * MB * (F32X ? 2 : 4) * 64 * 4;
+    constexpr int PS = PAIR ? 2 : 1;  // sources per wave
+    static_assert(!PAIR || NSRC == 2, "PAIR needs two sources");
+    constexpr int kRedBytes = NW * PS * MB * (F32X ? 2 : 4) * 64 * 4;
     constexpr int kXsHalves = 2 * ROWS * kPitch > kRedBytes / 2 ? 2 * ROWS * kPitch : kRedBytes / 2;
     __shared__ __align__(16) _Float16 xs[kXsHalves];
     _Float16 *const xs0 = xs, *const xs1 = xs + ROWS * kPitch;
@@ -189,7 +194,7 @@ __global__ __launch_bounds__(64 * NW) void i4mm_kernel(const void *__restrict__ 
     const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int t0 = (int)((long long)blockIdx.x * ntiles / gridDim.x);
     const int t1 = (int)((long long)(blockIdx.x + 1) * ntiles / gridDim.x);
-    const int tb = wave / (NSRC * S), src = (wave / S) % NSRC, slice = wave % S;
+    const int tb = PAIR ? wave / S : wave / (NSRC * S), src = PAIR ? 0 : (wave / S) % NSRC, slice = wave % S;
     const bool active = t0 + tb < t1;
     const int T = min(t0 + tb, ntiles - 1);
     const int G = K / GS;
@@ -198,18 +203,24 @@ __global__ __launch_bounds__(64 * NW) void i4mm_kernel(const void *__restrict__ 
     const int q = lane >> 4, r16 = lane & 15;
     const int n = min(kTileN * T + r16, N - 1);  // this lane's column (the last tile's padding repeats N - 1)
 
-    const uint32_t *qw = (NSRC == 2 && src) ? qw1 : qw0;
-    const uint16_t *sc = (NSRC == 2 && src) ? sc1 : sc0;
-    const uint32_t *qz = (NSRC == 2 && src) ? qz1 : qz0;
-    const bool has_z = qz != nullptr;
+    // per source the wave reads (PAIR: gate, up; otherwise its own source)
+    __amdgpu_buffer_rsrc_t rw[PS], rs[PS], rz[PS];
+    bool has_z[PS];
+#pragma unroll
+    for (int ps = 0; ps < PS; ++ps) {
+        const int sr = PAIR ? ps : src;
+        const uint32_t *qw = (NSRC == 2 && sr) ? qw1 : qw0;
+        const uint16_t *sc = (NSRC == 2 && sr) ? sc1 : sc0;
+        const uint32_t *qz = (NSRC == 2 && sr) ? qz1 : qz0;
+        has_z[ps] = qz != nullptr;
+        rw[ps] = __builtin_amdgcn_make_buffer_rsrc((void *)qw, (short)0, 0x7FFFFFFF, kRsrcWord3);
+        rs[ps] = __builtin_amdgcn_make_buffer_rsrc((void *)sc, (short)0, 0x7FFFFFFF, kRsrcWord3);
+        // without qzeros the zero loads read nothing (z = 8)
+        rz[ps] = __builtin_amdgcn_make_buffer_rsrc((void *)(has_z[ps] ? (const void *)qz : (const void *)sc), (short)0,
+                                                   0x7FFFFFFF, kRsrcWord3);
+    }
     const __amdgpu_buffer_rsrc_t rx = __builtin_amdgcn_make_buffer_rsrc((void *)x, (short)0, 0x7FFFFFFF, kRsrcWord3);
-    const __amdgpu_buffer_rsrc_t rw = __builtin_amdgcn_make_buffer_rsrc((void *)qw, (short)0, 0x7FFFFFFF, kRsrcWord3);
-    const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc((void *)sc, (short)0, 0x7FFFFFFF, kRsrcWord3);
     const __amdgpu_buffer_rsrc_t rp = __builtin_amdgcn_make_buffer_rsrc((void *)pe, (short)0, 0x7FFFFFFF, kRsrcWord3);
-    // without qzeros the zero loads read nothing (z = 8)
-    const __amdgpu_buffer_rsrc_t rz =
-        __builtin_amdgcn_make_buffer_rsrc((void *)(has_z ? (const void *)qz : (const void *)sc), (short)0, 0x7FFFFFFF,
-                                          kRsrcWord3);
 
     // ------------------------------------------------------------- x staging
     // Rows already in B order: the chunk is copied. With f32 x, threads
@@ -247,41 +258,46 @@ __global__ __launch_bounds__(64 * NW) void i4mm_kernel(const void *__restrict__ 
     // ------------------------------------------------------ weights, scales
     // Tiled words of group g: lane l's GS / 32 words at ((T G + g) 64 + l) GS / 32,
     // word 2 st + h = packed row GS / 8 g + 8 st + 2 (l / 16) + h.
-    Unit<GS> ur[3][GW];  // a ring of three chunks: loaded two chunks ahead
-    auto load_u = [&](Unit<GS> (&dst)[GW], int c) {
+    Unit<GS> ur[3][GW][PS];  // a ring of three chunks: loaded two chunks ahead
+    auto load_u = [&](Unit<GS> (&dsts)[GW][PS], int c) {
+#pragma unroll
+        for (int ps = 0; ps < PS; ++ps)
 #pragma unroll
         for (int gi = 0; gi < GW; ++gi) {
+            Unit<GS> &du = dsts[gi][ps];
             const int u = c * KCU + slice * GW + gi;
             const bool ok = active && u < units;
             if constexpr (GS == 64) {
                 const unsigned o0 = ok ? (unsigned)(((T * G + 2 * u) * 64 + lane) * 8) : kNoLoad;
-                const u32x2 a = __builtin_amdgcn_raw_buffer_load_b64(rw, o0, 0, 0);
-                const u32x2 b = __builtin_amdgcn_raw_buffer_load_b64(rw, o0, 64 * 8, 0);
-                dst[gi].w = u32x4{a.x, a.y, b.x, b.y};
+                const u32x2 a = __builtin_amdgcn_raw_buffer_load_b64(rw[ps], o0, 0, 0);
+                const u32x2 b = __builtin_amdgcn_raw_buffer_load_b64(rw[ps], o0, 64 * 8, 0);
+                du.w = u32x4{a.x, a.y, b.x, b.y};
             } else if constexpr (GS == 128) {
-                dst[gi].w = __builtin_amdgcn_raw_buffer_load_b128(
-                    rw, ok ? (unsigned)(((T * G + u) * 64 + lane) * 16) : kNoLoad, 0, 0);
+                du.w = __builtin_amdgcn_raw_buffer_load_b128(
+                    rw[ps], ok ? (unsigned)(((T * G + u) * 64 + lane) * 16) : kNoLoad, 0, 0);
             } else {
-                dst[gi].w = __builtin_amdgcn_raw_buffer_load_b128(
-                    rw, ok ? (unsigned)(((T * G + u / 2) * 64 + lane) * 32 + 16 * (u & 1)) : kNoLoad, 0, 0);
+                du.w = __builtin_amdgcn_raw_buffer_load_b128(
+                    rw[ps], ok ? (unsigned)(((T * G + u / 2) * 64 + lane) * 32 + 16 * (u & 1)) : kNoLoad, 0, 0);
             }
 #pragma unroll
             for (int j = 0; j < NG; ++j) {
                 const int g = GS == 64 ? 2 * u + j : (u * 128) / GS;
-                dst[gi].s[j] = __builtin_amdgcn_raw_buffer_load_b16(rs, ok ? (unsigned)(g * N + n) * 2u : kNoLoad, 0, 0);
-                dst[gi].z[j] = __builtin_amdgcn_raw_buffer_load_b32(
-                    rz, (ok && has_z) ? (unsigned)(g * (N / 8) + n / 8) * 4u : kNoLoad, 0, 0);
+                du.s[j] = __builtin_amdgcn_raw_buffer_load_b16(rs[ps], ok ? (unsigned)(g * N + n) * 2u : kNoLoad, 0, 0);
+                du.z[j] = __builtin_amdgcn_raw_buffer_load_b32(
+                    rz[ps], (ok && has_z[ps]) ? (unsigned)(g * (N / 8) + n / 8) * 4u : kNoLoad, 0, 0);
             }
         }
     };
 
     // Running sums: F32X: tokens TPB mb + 2 q + t2 (t2 < 2); f16: rows 16 mb + 4 q + i.
     constexpr int YV = F32X ? 2 : 4;
-    float ys[MB][YV];
+    float ys[PS][MB][YV];
 #pragma unroll
-    for (int mb = 0; mb < MB; ++mb)
+    for (int ps = 0; ps < PS; ++ps)
 #pragma unroll
-        for (int i = 0; i < YV; ++i) ys[mb][i] = 0.f;
+        for (int mb = 0; mb < MB; ++mb)
+#pragma unroll
+            for (int i = 0; i < YV; ++i) ys[ps][mb][i] = 0.f;
 
     // A wave without a tile (its workgroup owns fewer tiles than it has wave
     // groups) computes on: its sums are never used, a branch around the work
@@ -289,45 +305,57 @@ __global__ __launch_bounds__(64 * NW) void i4mm_kernel(const void *__restrict__ 
     // x reads all on one address (a broadcast) they take one LDS access
     // instead of eight from the other waves.
     const int amask = active ? -1 : 0;
-    auto compute = [&](const _Float16 *xs, const float *ps, const Unit<GS> (&src_u)[GW]) {
+    auto compute = [&](const _Float16 *xs, const float *pf, const Unit<GS> (&src_u)[GW][PS]) {
 #pragma unroll
         for (int gi = 0; gi < GW; ++gi) {
             const int ul = slice * GW + gi;  // unit within the chunk
             f32x2 pw[MB];                     // 2^e of this lane's two tokens per block
             if constexpr (F32X) {
 #pragma unroll
-                for (int mb = 0; mb < MB; ++mb) pw[mb] = *reinterpret_cast<const f32x2 *>(&ps[ul * 16 + TPB * mb + 2 * q]);
+                for (int mb = 0; mb < MB; ++mb) pw[mb] = *reinterpret_cast<const f32x2 *>(&pf[ul * 16 + TPB * mb + 2 * q]);
             }
 #pragma unroll
             for (int blk = 0; blk < 4 / EK; ++blk) {  // scaled blocks of EK steps
                 const int j = GS == 64 ? blk : 0;      // group of the block within the unit
-                const int z = has_z ? (int)((src_u[gi].z[j] >> (4 * (n & 7))) & 0xF) + zoff : 8;
-                const _Float16 zl = (_Float16)(1024 + z), zh = (_Float16)(-(64 + z));
-                const half2_t zlo = {zl, zl}, zhi = {zh, zh};
-                const float s = (float)__builtin_bit_cast(_Float16, (uint16_t)src_u[gi].s[j]);
-                f32x4 acc[MB];
+                half2_t zlo[PS], zhi[PS];
+                float s[PS];
+                f32x4 acc[PS][MB];
 #pragma unroll
-                for (int mb = 0; mb < MB; ++mb) acc[mb] = f32x4{0.f, 0.f, 0.f, 0.f};
+                for (int ps = 0; ps < PS; ++ps) {
+                    const int z = has_z[ps] ? (int)((src_u[gi][ps].z[j] >> (4 * (n & 7))) & 0xF) + zoff : 8;
+                    const _Float16 zl = (_Float16)(1024 + z), zh = (_Float16)(-(64 + z));
+                    zlo[ps] = half2_t{zl, zl};
+                    zhi[ps] = half2_t{zh, zh};
+                    s[ps] = (float)__builtin_bit_cast(_Float16, (uint16_t)src_u[gi][ps].s[j]);
+#pragma unroll
+                    for (int mb = 0; mb < MB; ++mb) acc[ps][mb] = f32x4{0.f, 0.f, 0.f, 0.f};
+                }
 #pragma unroll
                 for (int e = 0; e < EK; ++e) {
                     const int step = blk * EK + e;  // word 2 st + h
                     const int st = step >> 1, h = step & 1;
-                    const half8 b = word_to_b(src_u[gi].w[step], zlo, zhi);
+                    half8 b[PS];
+#pragma unroll
+                    for (int ps = 0; ps < PS; ++ps) b[ps] = word_to_b(src_u[gi][ps].w[step], zlo[ps], zhi[ps]);
                     const int kk = ul * 128 + 64 * st + 16 * q + 8 * h;
 #pragma unroll
                     for (int mb = 0; mb < MB; ++mb) {
                         const half8 a = *reinterpret_cast<const half8 *>(&xs[((16 * mb + r16) * kPitch + kk) & amask]);
-                        acc[mb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, acc[mb], 0, 0, 0);
+#pragma unroll
+                        for (int ps = 0; ps < PS; ++ps)
+                            acc[ps][mb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b[ps], acc[ps][mb], 0, 0, 0);
                     }
                 }
 #pragma unroll
+                for (int ps = 0; ps < PS; ++ps)
+#pragma unroll
                 for (int mb = 0; mb < MB; ++mb) {
                     if constexpr (F32X) {
-                        ys[mb][0] = __builtin_fmaf(s * pw[mb].x, acc[mb][0] + acc[mb][1], ys[mb][0]);
-                        ys[mb][1] = __builtin_fmaf(s * pw[mb].y, acc[mb][2] + acc[mb][3], ys[mb][1]);
+                        ys[ps][mb][0] = __builtin_fmaf(s[ps] * pw[mb].x, acc[ps][mb][0] + acc[ps][mb][1], ys[ps][mb][0]);
+                        ys[ps][mb][1] = __builtin_fmaf(s[ps] * pw[mb].y, acc[ps][mb][2] + acc[ps][mb][3], ys[ps][mb][1]);
                     } else {
 #pragma unroll
-                        for (int i = 0; i < 4; ++i) ys[mb][i] = __builtin_fmaf(s, acc[mb][i], ys[mb][i]);
+                        for (int i = 0; i < 4; ++i) ys[ps][mb][i] = __builtin_fmaf(s[ps], acc[ps][mb][i], ys[ps][mb][i]);
                     }
                 }
             }
@@ -368,11 +396,16 @@ __global__ __launch_bounds__(64 * NW) void i4mm_kernel(const void *__restrict__ 
 
     // Partial sums of the S waves of a tile (and source), added in slice order.
     float *red = reinterpret_cast<float *>(xs);
-    static_assert(NW * MB * YV * 64 * 4 == kRedBytes, "reduction buffer");
+    static_assert(NW * PS * MB * YV * 64 * 4 == kRedBytes, "reduction buffer");
+    // slot of (tile tb, source, slice): the wave index of the one-source layout
 #pragma unroll
-    for (int mb = 0; mb < MB; ++mb)
+    for (int ps = 0; ps < PS; ++ps) {
+        const int vw = (tb * NSRC + (PAIR ? ps : src)) * S + slice;
 #pragma unroll
-        for (int i = 0; i < YV; ++i) red[((wave * MB + mb) * YV + i) * 64 + lane] = ys[mb][i];
+        for (int mb = 0; mb < MB; ++mb)
+#pragma unroll
+            for (int i = 0; i < YV; ++i) red[((vw * MB + mb) * YV + i) * 64 + lane] = ys[ps][mb][i];
+    }
     lds_barrier();
     if (!active || slice != 0 || src != 0) return;
     const int nc = kTileN * T + r16;
@@ -395,11 +428,23 @@ __global__ __launch_bounds__(64 * NW) void i4mm_kernel(const void *__restrict__ 
 
 template <bool F32X, int NSRC, int MB, int GS>
 int launch_gs(st_context *ctx, const void *x, const float *pe, const uint32_t *const *qw, const uint16_t *const *sc,
-              const uint32_t *const *qz, int zoff, float *y, int M, int K, int N, int ntiles, int G, int wpt, int nw) {
+              const uint32_t *const *qz, int zoff, float *y, int M, int K, int N, int ntiles, int G, int wpt, int nw,
+              bool pair) {
     const dim3 grid(G);
-#define ST_I4MM(KCU_, GW_, NW_)                                                                                  \
-    hipLaunchKernelGGL((i4mm_kernel<F32X, NSRC, MB, GS, KCU_, GW_, NW_>), grid, dim3(64 * NW_), 0, ctx->stream, x, pe, \
-                       qw[0], sc[0], qz[0], qw[1], sc[1], qz[1], zoff, y, M, K, N, ntiles)
+#define ST_I4MM_P(KCU_, GW_, NW_, PAIR_)                                                                          \
+    hipLaunchKernelGGL((i4mm_kernel<F32X, NSRC, MB, GS, KCU_, GW_, NW_, PAIR_>), grid, dim3(64 * NW_), 0, ctx->stream, x, \
+                       pe, qw[0], sc[0], qz[0], qw[1], sc[1], qz[1], zoff, y, M, K, N, ntiles)
+#define ST_I4MM(KCU_, GW_, NW_) ST_I4MM_P(KCU_, GW_, NW_, false)
+    // gate/up with both sources in a wave: wpt is then waves per tile pair
+    if constexpr (NSRC == 2 && GS != 64) {  // (group 64 with two sources per wave spills)
+        if (pair) {
+            if (wpt >= 4)
+                ST_I4MM_P(4, 1, 12, true);
+            else
+                ST_I4MM_P(2, 1, 12, true);
+            return st::launch_check("i4mm_kernel");
+        }
+    }
     // waves per tile and source = 128-k units per chunk (one unit per wave):
     // 8 (1024-k chunks), 4 or 2. Group size 64 stops at 4: its 8-unit chunk
     // spilled 30 VGPRs inside the loop (one source, 16 tokens, 2560 x 6144:
@@ -422,6 +467,7 @@ int launch_gs(st_context *ctx, const void *x, const float *pe, const uint32_t *c
             ST_I4MM(2, 1, 16);
     }
 #undef ST_I4MM
+#undef ST_I4MM_P
     return st::launch_check("i4mm_kernel");
 }
 
@@ -442,22 +488,24 @@ __global__ __launch_bounds__(256) void i4mm_gather_kernel(const uint16_t *__rest
 template <bool F32X, int NSRC, int MB>
 int launch_mb(st_context *ctx, const void *x, const float *pe, const uint32_t *const *qw, const uint16_t *const *sc,
               const uint32_t *const *qz, int zoff, float *y, int M, int K, int N, int gs, int ntiles, int G, int wpt,
-              int nw) {
+              int nw, bool pair) {
     switch (gs) {
-        case 64: return launch_gs<F32X, NSRC, MB, 64>(ctx, x, pe, qw, sc, qz, zoff, y, M, K, N, ntiles, G, wpt, nw);
-        case 128: return launch_gs<F32X, NSRC, MB, 128>(ctx, x, pe, qw, sc, qz, zoff, y, M, K, N, ntiles, G, wpt, nw);
-        default: return launch_gs<F32X, NSRC, MB, 256>(ctx, x, pe, qw, sc, qz, zoff, y, M, K, N, ntiles, G, wpt, nw);
+        case 64: return launch_gs<F32X, NSRC, MB, 64>(ctx, x, pe, qw, sc, qz, zoff, y, M, K, N, ntiles, G, wpt, nw, pair);
+        case 128:
+            return launch_gs<F32X, NSRC, MB, 128>(ctx, x, pe, qw, sc, qz, zoff, y, M, K, N, ntiles, G, wpt, nw, pair);
+        default:
+            return launch_gs<F32X, NSRC, MB, 256>(ctx, x, pe, qw, sc, qz, zoff, y, M, K, N, ntiles, G, wpt, nw, pair);
     }
 }
 
 template <bool F32X, int NSRC>
 int launch_src(st_context *ctx, const void *x, const float *pe, const uint32_t *const *qw, const uint16_t *const *sc,
                const uint32_t *const *qz, int zoff, float *y, int M, int K, int N, int gs, int ntiles, int G, int wpt,
-               int nw) {
+               int nw, bool pair) {
     // tokens per 16-row block: 8 (f32 x: hi and lo rows) or 16
     const int mb = (M * (F32X ? 2 : 1) + 15) / 16;
-    return mb <= 1 ? launch_mb<F32X, NSRC, 1>(ctx, x, pe, qw, sc, qz, zoff, y, M, K, N, gs, ntiles, G, wpt, nw)
-                   : launch_mb<F32X, NSRC, 2>(ctx, x, pe, qw, sc, qz, zoff, y, M, K, N, gs, ntiles, G, wpt, nw);
+    return mb <= 1 ? launch_mb<F32X, NSRC, 1>(ctx, x, pe, qw, sc, qz, zoff, y, M, K, N, gs, ntiles, G, wpt, nw, pair)
+                   : launch_mb<F32X, NSRC, 2>(ctx, x, pe, qw, sc, qz, zoff, y, M, K, N, gs, ntiles, G, wpt, nw, pair);
 }
 
 }  // namespace
@@ -480,7 +528,20 @@ int int4_mm_f16(st_context *ctx, const void *x, bool x_f32, const int32_t *perm,
     if (wpt * nsrc * tbmax > kWaves) return fail(ST_ERR_SHAPE, "int4_mm_f16: %d tiles per workgroup", tbmax);
     // 12-wave workgroups when the tiles use at most 12 waves (gate/up with 3
     // tile pairs per workgroup): idle waves would still issue the loop's VALU
-    const int nw = (wpt <= 4 && wpt * nsrc * tbmax <= 12 && tune(ctx, ST_TUNE_I4MM_WAVES, 0) != 16) ? 12 : 16;
+    int nw = (wpt <= 4 && wpt * nsrc * tbmax <= 12 && tune(ctx, ST_TUNE_I4MM_WAVES, 0) != 16) ? 12 : 16;
+    // gate/up: both sources in one wave when the tile pairs then use 10-12
+    // of 12 waves (wpt becomes waves per tile pair: 3 pairs of 4 waves, or
+    // 5-6 pairs of 2)
+    bool pair = false;
+    if (nsrc == 2 && gs != 64 && tune(ctx, ST_TUNE_I4MM_PAIR, 1) != 0 && tune(ctx, ST_TUNE_I4MM_WAVES, 0) != 16) {
+        int wpp = 2;
+        while (wpp < 4 && 2 * wpp * tbmax <= 12) wpp *= 2;
+        if (wpp * tbmax >= 10 && wpp * tbmax <= 12) {
+            pair = true;
+            wpt = wpp;
+            nw = 12;
+        }
+    }
     const void *xa = x;
     const float *pe = nullptr;
     if (x_f32) {  // the pre-pass writes [2M, K] f16 rows and [M, K / 128] factors into the workspace
@@ -504,10 +565,10 @@ int int4_mm_f16(st_context *ctx, const void *x, bool x_f32, const int32_t *perm,
         xa = xg;
     }
     if (nsrc == 2)
-        return x_f32 ? launch_src<true, 2>(ctx, xa, pe, qw, sc, qz, zoff, y, M, K, N, gs, ntiles, G, wpt, nw)
-                     : launch_src<false, 2>(ctx, xa, pe, qw, sc, qz, zoff, y, M, K, N, gs, ntiles, G, wpt, nw);
-    return x_f32 ? launch_src<true, 1>(ctx, xa, pe, qw, sc, qz, zoff, y, M, K, N, gs, ntiles, G, wpt, nw)
-                 : launch_src<false, 1>(ctx, xa, pe, qw, sc, qz, zoff, y, M, K, N, gs, ntiles, G, wpt, nw);
+        return x_f32 ? launch_src<true, 2>(ctx, xa, pe, qw, sc, qz, zoff, y, M, K, N, gs, ntiles, G, wpt, nw, pair)
+                     : launch_src<false, 2>(ctx, xa, pe, qw, sc, qz, zoff, y, M, K, N, gs, ntiles, G, wpt, nw, pair);
+    return x_f32 ? launch_src<true, 1>(ctx, xa, pe, qw, sc, qz, zoff, y, M, K, N, gs, ntiles, G, wpt, nw, pair)
+                 : launch_src<false, 1>(ctx, xa, pe, qw, sc, qz, zoff, y, M, K, N, gs, ntiles, G, wpt, nw, pair);
 }
 
 }  // namespace st
