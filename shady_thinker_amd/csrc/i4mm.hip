@@ -16,7 +16,9 @@
 //    matvec kernels grow their per-token staging and epilogue work with M).
 //  * Work split as in i8mm.hip: one workgroup per CU owns a run of 16-column
 //    tiles (gate/up: the gate and up tiles of each); S waves per tile each
-//    take one 128-k unit of every S-unit chunk. x is copied per chunk into
+//    take one 128-k unit of every S-unit chunk (gate/up in PAIR mode: of
+//    both the gate and the up tile). 16 waves per workgroup, or 12 when its
+//    tiles use at most 12. x is copied per chunk into
 //    LDS (double buffered, one chunk ahead); each wave keeps a ring of three
 //    chunks of weights, scales and zeros, two in flight while it computes
 //    one. Partial sums meet in LDS in a fixed order.
