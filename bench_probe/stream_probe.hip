@@ -6,6 +6,7 @@
 // the fastest a launch of that size can read its bytes on the same box.
 // Not part of the product path (a separate library, libshady_probe.so, loaded
 // only by the benchmark); it has no reference counterpart.
+#include <hip/hip_ext.h>
 #include <hip/hip_runtime.h>
 
 #include <cstddef>
@@ -61,18 +62,23 @@ __global__ __launch_bounds__(1024) void stream_read_kernel(const u32x4 *__restri
 }  // namespace
 
 // grid workgroups of `block` threads (64..1024, a multiple of 64); sink holds
-// at least `grid` words.
-extern "C" int stp_read(const void *buf, size_t bytes, unsigned *sink, int grid, int block, int mode, void *stream) {
+// at least `grid` words. start / stop (hipEvent_t, or NULL) are stamped with
+// the kernel's own start and end (hipExtLaunchKernel), as the library's
+// kernels are timed.
+extern "C" int stp_read(const void *buf, size_t bytes, unsigned *sink, int grid, int block, int mode, void *stream,
+                        void *start, void *stop) {
     if (!buf || !sink || grid <= 0 || block < 64 || block > 1024 || block % 64 || bytes % 16 || (uintptr_t)buf % 16 ||
         mode < 0 || mode > 2)
         return 1;
     const u32x4 *p = reinterpret_cast<const u32x4 *>(buf);
     const hipStream_t s = (hipStream_t)stream;
+    const hipEvent_t e0 = (hipEvent_t)start, e1 = (hipEvent_t)stop;
+    const size_t n16 = bytes / 16;
     if (mode == 0)
-        hipLaunchKernelGGL(stream_read_kernel<0>, dim3(grid), dim3(block), 0, s, p, bytes / 16, sink);
+        hipExtLaunchKernelGGL(stream_read_kernel<0>, dim3(grid), dim3(block), 0, s, e0, e1, 0u, p, n16, sink);
     else if (mode == 1)
-        hipLaunchKernelGGL(stream_read_kernel<1>, dim3(grid), dim3(block), 0, s, p, bytes / 16, sink);
+        hipExtLaunchKernelGGL(stream_read_kernel<1>, dim3(grid), dim3(block), 0, s, e0, e1, 0u, p, n16, sink);
     else
-        hipLaunchKernelGGL(stream_read_kernel<2>, dim3(grid), dim3(block), 0, s, p, bytes / 16, sink);
+        hipExtLaunchKernelGGL(stream_read_kernel<2>, dim3(grid), dim3(block), 0, s, e0, e1, 0u, p, n16, sink);
     return hipGetLastError() == hipSuccess ? 0 : 2;
 }

@@ -121,6 +121,23 @@ typedef enum {
 int st_context_set_tune(st_context *ctx, int knob, int value);
 int st_context_get_tune(st_context *ctx, int knob, int *value);
 
+/* Kernel timing, in place of the reference's wgpu timestamp-less submits
+ * (src/gpu.rs:188-242 has no timing): arms two hipEvent_t (created by the
+ * caller, passed as void*) on the context. The next kernel launch records
+ * `start` at its kernel's start; every launch records `stop` at its kernel's
+ * end (hipExtLaunchKernel's dispatch timestamps, the duration a profiler
+ * reports, without the gap between launches), so over one entry-point call
+ * the pair spans its kernels. Stays armed until called again; NULL, NULL
+ * disarms. Not for stream capture. */
+int st_context_set_timing_events(st_context *ctx, void *start, void *stop);
+
+/* Pins the context's workspace (delta +1) or releases a pin (-1): a captured
+ * HIP graph holds kernels that point into the workspace, so while any pin is
+ * held st_context_reserve_workspace refuses to reallocate it. DecoderStack's
+ * capture (the host mirror of src/model.rs:669-969) takes one for the life
+ * of its graph; no reference counterpart (wgpu has no graphs). */
+int st_context_pin_workspace(st_context *ctx, int delta);
+
 /* Replaces GpuContext::create_buffer / create_storage_buffer (src/gpu.rs:80-103): device
  * allocation, size rounded up to 4 bytes, 256-byte aligned. */
 int st_alloc(st_context *ctx, size_t bytes, void **out);
@@ -177,7 +194,12 @@ int st_gptq_i4_matvec(st_context *ctx, const void *x, int x_dtype,
  * ST_NOALLOC_SCRATCH_BYTES that the library holds on every GPU it runs on,
  * from the context's creation until the process ends, instead of the
  * context workspace. Allocates nothing. A call whose scratch would exceed
- * the array fails with ST_ERR_WORKSPACE and launches nothing. Every call on
+ * the array fails with ST_ERR_WORKSPACE and launches nothing. The check is
+ * conservative: for f32 x (and for f16 x under act-order) it counts the
+ * f16-MFMA kernel's split rows of one 16-token block, 4 M K + M K / 32 bytes
+ * (f16 x with perm: 2 M K), with M capped at 16, whichever kernel the call
+ * then takes; split-K partials are not counted (they shrink or go unsplit
+ * to fit the array). Every call on
  * one GPU shares that GPU's array (nothing in it needs to start at zero;
  * each call overwrites what it reads): calls that overlap on one GPU (other
  * streams or contexts) race. */

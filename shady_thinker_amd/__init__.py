@@ -18,6 +18,6 @@ from .model import (  # noqa: F401
     int8_matvec,
     linear,
 )
-from .layer import DecoderLinears, DecoderStack, StackBuffers, StackGraph  # noqa: F401
+from .layer import DecoderLinears, DecoderStack, DeltaNetLinears, StackBuffers, StackGraph, layer_from_linears  # noqa: F401
 from .loader import load_gptq_checkpoint, read_gptq_checkpoint  # noqa: F401
 from .weights import GptqWeight, Int8Weight, QuantConfig  # noqa: F401

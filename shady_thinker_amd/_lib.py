@@ -57,6 +57,8 @@ _SIGNATURES = {
     "st_context_destroy": (_I, [_P]),
     "st_context_set_tune": (_I, [_P, _I, _I]),
     "st_context_get_tune": (_I, [_P, _I, ctypes.POINTER(_I)]),
+    "st_context_set_timing_events": (_I, [_P, _P, _P]),
+    "st_context_pin_workspace": (_I, [_P, _I]),
     "st_alloc": (_I, [_P, _SZ, ctypes.POINTER(_P)]),
     "st_free": (_I, [_P, _P]),
     "st_upload": (_I, [_P, _P, _P, _SZ]),

@@ -16,9 +16,6 @@ ROOT = os.path.dirname(HERE)
 CSRC = os.path.join(HERE, "csrc")
 OBJ = os.path.join(HERE, "_build")
 LIB = os.path.join(HERE, "libshady_hip.so")
-# The benchmark's plain streaming-read probe: its own library, never linked
-# into or loaded by the product.
-PROBE_SRC, PROBE_LIB = "stream_probe.hip", os.path.join(HERE, "libshady_probe.so")
 SOURCES = [
     "runtime.hip", "qmv.hip", "qmv_i4_p0.hip", "qmv_i4_p1.hip", "qmv_i4t_p0.hip", "qmv_i4t_p1.hip", "qmv_i8.hip", "qmv_i8t.hip",
     "i8mm.hip", "i4mm.hip", "dequant.hip", "gemm.hip", "bf16mv.hip",
@@ -69,23 +66,7 @@ def build(verbose: bool = True) -> str:
     os.replace(tmp, LIB)
     if verbose:
         print(f"built {LIB}")
-    build_probe(verbose)
     return LIB
-
-
-def build_probe(verbose: bool = True) -> str:
-    """Compile and link libshady_probe.so (bench.py's plain-stream ceiling)."""
-    os.makedirs(OBJ, exist_ok=True)
-    obj = _compile(PROBE_SRC)
-    tmp = PROBE_LIB + ".tmp"
-    r = subprocess.run([HIPCC, "--offload-arch=gfx950", "-shared", "-fPIC", obj, "-o", tmp], capture_output=True,
-                       text=True)
-    if r.returncode != 0:
-        raise RuntimeError(f"link failed:\n{r.stdout}\n{r.stderr}")
-    os.replace(tmp, PROBE_LIB)
-    if verbose:
-        print(f"built {PROBE_LIB}")
-    return PROBE_LIB
 
 
 if __name__ == "__main__":

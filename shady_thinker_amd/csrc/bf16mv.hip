@@ -138,7 +138,7 @@ int launch(st_context *ctx, const void *x, const uint16_t *w, float *y, int M, i
     auto kern = bf16mv_kernel<MT, F16X>;
     if (lds > 64 * 1024)
         ST_HIP(hipFuncSetAttribute((const void *)kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds));
-    hipLaunchKernelGGL(kern, dim3(wgs), dim3(kThreads), lds, ctx->stream, x, w, y, M, K, N, gpw);
+    st::launch(ctx, kern, dim3(wgs), dim3(kThreads), lds, x, w, y, M, K, N, gpw);
     return st::launch_check("bf16mv_kernel");
 }
 

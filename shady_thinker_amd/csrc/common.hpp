@@ -2,6 +2,7 @@
 // argument checks. gfx950 (CDNA4) only.
 #pragma once
 
+#include <hip/hip_ext.h>
 #include <hip/hip_runtime.h>
 
 #include <cstdarg>
@@ -21,6 +22,7 @@ struct st_context {
     // what it uses; calls on one context are ordered by its stream).
     float *ws = nullptr;
     size_t ws_bytes = 0;
+    int ws_pins = 0;  // captured graphs that point into ws (st_context_pin_workspace)
     // split-K counters of the decode kernels (kSplitCounters words, zero
     // between calls: the last slice of each tile group clears its own)
     unsigned *split_counters = nullptr;
@@ -29,6 +31,9 @@ struct st_context {
     void *scratch = nullptr;
     // kernel-path overrides (st_tune); -1 = automatic
     int tune[ST_TUNE_COUNT];
+    // timing events (st_context_set_timing_events): the next launch records
+    // t_start at its kernel's start, every launch records t_stop at its end
+    hipEvent_t t_start = nullptr, t_stop = nullptr;
     st_context() {
         for (int &t : tune) t = -1;
     }
@@ -75,6 +80,23 @@ inline int launch_check(const char *what) {
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return hip_fail(e, what);
     return ST_OK;
+}
+
+// Every kernel launch of the library. With timing events armed on the
+// context, the launch goes through hipExtLaunchKernel, which stamps the events
+// with the kernel's own start and end (the dispatch's timestamps, as a
+// profiler sees them, without the gap between launches): t_start on the first
+// launch after arming, t_stop on every launch, so that over a call of several
+// launches the pair spans all of them.
+template <typename F, typename... Args>
+inline void launch(st_context *ctx, F kernel, dim3 grid, dim3 block, size_t lds, Args... args) {
+    if (ctx->t_start || ctx->t_stop) {
+        hipExtLaunchKernelGGL(kernel, grid, block, (std::uint32_t)lds, ctx->stream, ctx->t_start, ctx->t_stop, 0u,
+                              args...);
+        ctx->t_start = nullptr;
+    } else {
+        hipLaunchKernelGGL(kernel, grid, block, lds, ctx->stream, args...);
+    }
 }
 
 // Multi-token INT8 matvec with f16 x on f16 MFMA (i8mm.hip); the caller

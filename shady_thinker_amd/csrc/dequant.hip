@@ -71,10 +71,10 @@ int st_gptq_i4_dequant(st_context *ctx, const uint32_t *qweight, const uint16_t 
     const int zoff = (flags & ST_FLAG_ZEROS_PLUS_ONE) ? 1 : 0;
     dim3 grid((unsigned)((nwords + 255) / 256)), block(256);
     if (out_dtype == ST_F32)
-        hipLaunchKernelGGL(dequant_kernel<ST_F32>, grid, block, 0, ctx->stream, qweight, scales, qzeros, g_idx, out, K, N,
+        st::launch(ctx, dequant_kernel<ST_F32>, grid, block, 0, qweight, scales, qzeros, g_idx, out, K, N,
                            group_size, zoff);
     else if (out_dtype == ST_BF16)
-        hipLaunchKernelGGL(dequant_kernel<ST_BF16>, grid, block, 0, ctx->stream, qweight, scales, qzeros, g_idx, out, K, N,
+        st::launch(ctx, dequant_kernel<ST_BF16>, grid, block, 0, qweight, scales, qzeros, g_idx, out, K, N,
                            group_size, zoff);
     else
         return st::fail(ST_ERR_INVALID, "st_gptq_i4_dequant: out_dtype %d (F32 or BF16)", out_dtype);
@@ -108,7 +108,7 @@ int st_gptq_i4_act_order(st_context *ctx, const uint32_t *qweight, const int32_t
     for (int k = 0; k < K; ++k) perm[start[gi[k]]++] = k;
     ST_HIP(hipMemcpyAsync(perm_out, perm.data(), sizeof(int32_t) * K, hipMemcpyHostToDevice, ctx->stream));
     const long long nwords = (long long)(K / 8) * N;
-    hipLaunchKernelGGL(act_order_gather, dim3((unsigned)((nwords + 255) / 256)), dim3(256), 0, ctx->stream, qweight,
+    st::launch(ctx, act_order_gather, dim3((unsigned)((nwords + 255) / 256)), dim3(256), 0, qweight,
                        perm_out, qweight_out, K, N);
     if (int rc = st::launch_check("act_order_gather")) return rc;
     ST_HIP(hipStreamSynchronize(ctx->stream));

@@ -661,11 +661,11 @@ int launch_cb(st_context *ctx, const GemmArgs &g, const Split &sp) {
     const int T = ((g.M + BM - 1) / BM) * ((g.N + 32 * CBL * WN - 1) / (32 * CBL * WN)) * (g.C1 ? 2 : 1);
     const dim3 grid(T * sp.S);
     if (g.f16out)
-        hipLaunchKernelGGL((gemm_kernel<GS, TILED, true, CBL, I8>), grid, dim3(kThreads), 0, ctx->stream, g.A, g.qw, g.sc,
+        st::launch(ctx, (gemm_kernel<GS, TILED, true, CBL, I8>), grid, dim3(kThreads), 0, g.A, g.qw, g.sc,
                            g.qz, g.zoff, g.rsc, g.chs, g.C, g.M, g.K, g.N, sp.kps, sp.part, vec_ok(g, sp), g.qw1, g.sc1,
                            g.qz1, g.C1);
     else
-        hipLaunchKernelGGL((gemm_kernel<GS, TILED, false, CBL, I8>), grid, dim3(kThreads), 0, ctx->stream, g.A, g.qw, g.sc,
+        st::launch(ctx, (gemm_kernel<GS, TILED, false, CBL, I8>), grid, dim3(kThreads), 0, g.A, g.qw, g.sc,
                            g.qz, g.zoff, g.rsc, g.chs, g.C, g.M, g.K, g.N, sp.kps, sp.part, vec_ok(g, sp), g.qw1, g.sc1,
                            g.qz1, g.C1);
     return st::launch_check("gemm_kernel");
@@ -682,9 +682,9 @@ int launch_gs(st_context *ctx, const GemmArgs &g, int cb, const Split &sp) {
         const size_t MN = (size_t)M * N;
         const dim3 rg((unsigned)((MN / 4 + 255) / 256));
         if (f16out)
-            hipLaunchKernelGGL(splitk_reduce_kernel<true>, rg, dim3(256), 0, ctx->stream, sp.part, C, MN, sp.S);
+            st::launch(ctx, splitk_reduce_kernel<true>, rg, dim3(256), 0, sp.part, C, MN, sp.S);
         else
-            hipLaunchKernelGGL(splitk_reduce_kernel<false>, rg, dim3(256), 0, ctx->stream, sp.part, C, MN, sp.S);
+            st::launch(ctx, splitk_reduce_kernel<false>, rg, dim3(256), 0, sp.part, C, MN, sp.S);
         return st::launch_check("splitk_reduce_kernel");
     }
     return ST_OK;
@@ -779,7 +779,7 @@ int gemm_impl(const char *fn, st_context *ctx, const uint16_t *a, const uint16_t
     if (perm && !st::aligned16(perm)) return st::fail(ST_ERR_ALIGN, "%s: perm must be 16-byte aligned", fn);
     _Float16 *A = reinterpret_cast<_Float16 *>(ctx->ws);
     float *rsc = u ? reinterpret_cast<float *>(reinterpret_cast<char *>(ctx->ws) + rsc_off) : nullptr;
-    hipLaunchKernelGGL(prep_a_kernel, dim3(M), dim3(256), (size_t)K * sizeof(_Float16), ctx->stream,
+    st::launch(ctx, prep_a_kernel, dim3(M), dim3(256), (size_t)K * sizeof(_Float16),
                        reinterpret_cast<const _Float16 *>(a), reinterpret_cast<const _Float16 *>(u), perm, A, rsc, K);
     if (int rc = st::launch_check("prep_a_kernel")) return rc;
     GemmArgs g{A, qweight, scales, qzeros, (flags & ST_FLAG_ZEROS_PLUS_ONE) ? 1 : 0, rsc, nullptr, c,
@@ -788,12 +788,16 @@ int gemm_impl(const char *fn, st_context *ctx, const uint16_t *a, const uint16_t
         return (flags & ST_FLAG_TILED) ? launch_tiled<true>(ctx, ga, group_size, cb, sp)
                                        : launch_tiled<false>(ctx, ga, group_size, cb, sp);
     };
+    const int cb = pick_cb(ctx, M, N, false);
+    const Split sp = plan_split(ctx, M, K, N, cb, need);
     if (w1) {
-        // Both weights' tiles in one grid when that needs no split-K (the
-        // partials are laid out for one C); otherwise two launches on A.
+        // Both weights' tiles in one grid when neither that grid nor one
+        // weight's alone splits K (the partials are laid out for one C, and
+        // a split changes the order of the f32 sums, so the results would no
+        // longer be those of st_gptq_i4_gemm); otherwise two launches on A.
         const int cb2 = pick_cb(ctx, M, 2 * N, false);
         const Split sp2 = plan_split(ctx, M, K, 2 * N, cb2, need);
-        if (sp2.S == 1) {
+        if (sp2.S == 1 && sp.S == 1) {
             GemmArgs g2 = g;
             g2.qw1 = w1->qweight;
             g2.sc1 = w1->scales;
@@ -802,8 +806,6 @@ int gemm_impl(const char *fn, st_context *ctx, const uint16_t *a, const uint16_t
             return run(g2, cb2, sp2);
         }
     }
-    const int cb = pick_cb(ctx, M, N, false);
-    const Split sp = plan_split(ctx, M, K, N, cb, need);
     if (int rc = run(g, cb, sp)) return rc;
     if (!w1) return ST_OK;
     GemmArgs g1 = g;

@@ -434,7 +434,7 @@ int launch_gs(st_context *ctx, const void *x, const float *pe, const uint32_t *c
               bool pair) {
     const dim3 grid(G);
 #define ST_I4MM_P(KCU_, GW_, NW_, PAIR_)                                                                          \
-    hipLaunchKernelGGL((i4mm_kernel<F32X, NSRC, MB, GS, KCU_, GW_, NW_, PAIR_>), grid, dim3(64 * NW_), 0, ctx->stream, x, \
+    st::launch(ctx, (i4mm_kernel<F32X, NSRC, MB, GS, KCU_, GW_, NW_, PAIR_>), grid, dim3(64 * NW_), 0, x, \
                        pe, qw[0], sc[0], qz[0], qw[1], sc[1], qz[1], zoff, y, M, K, N, ntiles)
 #define ST_I4MM(KCU_, GW_, NW_) ST_I4MM_P(KCU_, GW_, NW_, false)
     // gate/up with both sources in a wave: wpt is then waves per tile pair
@@ -553,7 +553,7 @@ int int4_mm_f16(st_context *ctx, const void *x, bool x_f32, const int32_t *perm,
         _Float16 *xp = reinterpret_cast<_Float16 *>(ctx->ws);
         pe = reinterpret_cast<const float *>(reinterpret_cast<const char *>(ctx->ws) + xbytes);
         const int groups = M * (K / 128);
-        hipLaunchKernelGGL(i4mm_prep_kernel, dim3((groups + 15) / 16), dim3(256), 0, ctx->stream,
+        st::launch(ctx, i4mm_prep_kernel, dim3((groups + 15) / 16), dim3(256), 0,
                            static_cast<const float *>(x), perm, xp, const_cast<float *>(pe), M, K);
         if (int rc = launch_check("i4mm_prep_kernel")) return rc;
         xa = xp;
@@ -561,8 +561,7 @@ int int4_mm_f16(st_context *ctx, const void *x, bool x_f32, const int32_t *perm,
         const size_t xbytes = (size_t)M * K * 2;
         if (!ctx->ws || xbytes > ctx->ws_bytes) return fail(ST_ERR_WORKSPACE, "int4_mm_f16: workspace below %zu B", xbytes);
         uint16_t *xg = reinterpret_cast<uint16_t *>(ctx->ws);
-        hipLaunchKernelGGL(i4mm_gather_kernel, dim3((unsigned)(((size_t)M * K / 8 + 255) / 256)), dim3(256), 0,
-                           ctx->stream, static_cast<const uint16_t *>(x), perm, xg, M, K);
+        st::launch(ctx, i4mm_gather_kernel, dim3((unsigned)(((size_t)M * K / 8 + 255) / 256)), dim3(256), 0, static_cast<const uint16_t *>(x), perm, xg, M, K);
         if (int rc = launch_check("i4mm_gather_kernel")) return rc;
         xa = xg;
     }

@@ -183,9 +183,9 @@ int launch_mb(st_context *ctx, const _Float16 *x, const int8_t *w, const float *
               int ntiles, int G, int gw) {
     const dim3 grid(G), block(kThreads);
     switch (gw) {
-        case 1: hipLaunchKernelGGL((i8mm_kernel<MB, 1>), grid, block, 0, ctx->stream, x, w, scale, y, M, K, N, ntiles); break;
-        case 2: hipLaunchKernelGGL((i8mm_kernel<MB, 2>), grid, block, 0, ctx->stream, x, w, scale, y, M, K, N, ntiles); break;
-        default: hipLaunchKernelGGL((i8mm_kernel<MB, 4>), grid, block, 0, ctx->stream, x, w, scale, y, M, K, N, ntiles); break;
+        case 1: st::launch(ctx, (i8mm_kernel<MB, 1>), grid, block, 0, x, w, scale, y, M, K, N, ntiles); break;
+        case 2: st::launch(ctx, (i8mm_kernel<MB, 2>), grid, block, 0, x, w, scale, y, M, K, N, ntiles); break;
+        default: st::launch(ctx, (i8mm_kernel<MB, 4>), grid, block, 0, x, w, scale, y, M, K, N, ntiles); break;
     }
     return st::launch_check("i8mm_kernel");
 }

@@ -259,7 +259,7 @@ int st_gptq_i4_repack(st_context *ctx, const uint32_t *qweight, uint32_t *qweigh
         return st::fail(ST_ERR_ALIGN, "st_gptq_i4_repack: output must be 16-byte aligned");
     const int ntiles = (N + kTileN - 1) / kTileN;
     const long long total = (long long)ntiles * (K / group_size) * 64 * (group_size / 32);
-    hipLaunchKernelGGL(repack_kernel, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, ctx->stream, qweight,
+    st::launch(ctx, repack_kernel, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, qweight,
                        qweight_tiled, K, N, group_size, ntiles);
     return st::launch_check("repack_kernel");
 }
@@ -276,7 +276,7 @@ int st_int8_repack(st_context *ctx, const int8_t *w, int8_t *w_tiled, int K, int
         return st::fail(ST_ERR_ALIGN, "st_int8_repack: w and w_tiled must be 16-byte aligned");
     const int ntiles = (N + kTileN - 1) / kTileN;
     const long long total = (long long)ntiles * (K / 128) * 128;
-    hipLaunchKernelGGL(repack8_kernel, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, ctx->stream, w, w_tiled, K,
+    st::launch(ctx, repack8_kernel, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, w, w_tiled, K,
                        N, ntiles);
     return st::launch_check("repack8_kernel");
 }

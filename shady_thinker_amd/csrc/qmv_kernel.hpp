@@ -308,17 +308,6 @@ __device__ __forceinline__ void quantize_item(float (&v)[16], bool ok, u32x4 *ds
 
 constexpr int kMaxKSplit = 16;  // CHK split-K: most K slices
 
-// Per-wave phase timestamps for probe builds (-DST_STREAM_TRACE), used by
-// both decode kernels; compiled out otherwise.
-#ifdef ST_STREAM_TRACE
-__device__ unsigned long long st_stream_trace[2048 * 16 * 12];
-#define ST_TR(k) \
-    if (lane == 0 && blockIdx.x < 2048) \
-    st_stream_trace[((size_t)blockIdx.x * 16 + wave) * 12 + (k)] = __builtin_amdgcn_s_memrealtime()
-#else
-#define ST_TR(k)
-#endif
-
 // s_waitcnt vmcnt(0) (expcnt and lgkmcnt left at their maxima).
 __device__ __forceinline__ void wait_vm_all() { __builtin_amdgcn_s_waitcnt(0x0F70); }
 
@@ -738,14 +727,11 @@ __global__ __launch_bounds__((64 * (CM == 3 ? kChunkWaves<NSRC, MB> : kMaxWavesF
     // once. Nothing is in flight across the branch. Fallback: x first (loads complete in issue order),
     // then the ring, then the staging.
     const int cs0 = (COOP && !PW) ? 0 : u0;
-    ST_TR(0);
     if (COOP && !PW && wave < NS) {
         xload(cs0);
         wait_vm_all();
-        ST_TR(1);
         stage(cs0);
     }
-    ST_TR(2);
     if (PW) xload(cs0);  // (a wave without groups has no items: uniform skip inside)
     // per-wave staging: every wave's x loads enter the CU's memory queue
     // before any weight load (the waves of a workgroup start up to ~0.6 us
@@ -795,7 +781,6 @@ __global__ __launch_bounds__((64 * (CM == 3 ? kChunkWaves<NSRC, MB> : kMaxWavesF
         // flight (vmcnt(0)), i.e. for the ring. The asm's memory clobber
         // keeps the compiler from moving LDS accesses across it.
         asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
-        ST_TR(3);
         // the rest of the ring, after the barrier: issuing it can stall while
         // the CU's memory queue is full, and that must not hold up the barrier
 #pragma unroll
@@ -818,7 +803,6 @@ __global__ __launch_bounds__((64 * (CM == 3 ? kChunkWaves<NSRC, MB> : kMaxWavesF
                     ui = 0;
                     next_chunk(u);
                 }
-                if (u == u0) ST_TR(7);
                 compute(ring[d], u, ui);
                 ++ui;
                 load_unit(ring[d], min(u + D, u1 - 1), u + D < u1);
@@ -841,21 +825,18 @@ __global__ __launch_bounds__((64 * (CM == 3 ? kChunkWaves<NSRC, MB> : kMaxWavesF
     }
 
     // ------------------------------------------- reduce the waves, write y
-    ST_TR(4);
     float *red = reinterpret_cast<float *>(smem + (COOP ? (size_t)p.wave_lds : (size_t)NW * p.wave_lds));
 #pragma unroll
     for (int src = 0; src < NSRC; ++src)
 #pragma unroll
         for (int mb = 0; mb < MB; ++mb) red[((wave * NSRC + src) * MB + mb) * 64 + lane] = tot[src][mb];
     __syncthreads();
-    ST_TR(5);
     // split K with the reduction fused (p.cnt): every slice writes its
     // partial through to memory (sc0 sc1 stores, completed before the
     // counter), the last of the tile group's slices to count in adds them in
     // slice order and writes y. Nobody waits for anybody.
     const bool fused = CHK && KS > 1 && p.cnt != nullptr;
     if (!fused && wave >= TB) {
-        ST_TR(6);
         return;
     }  // wave j (< TB) sums the K slices of tile t0 + j, in slice order
     const int n = (t0 + wave) * kTileN + c;  // column of tile t0 + wave
@@ -901,6 +882,21 @@ __global__ __launch_bounds__((64 * (CM == 3 ? kChunkWaves<NSRC, MB> : kMaxWavesF
         if constexpr (is_i8(FMT)) out *= p.scale8[n];
         p.y[(size_t)m * N + n] = out;
     }
+    // Why the slices' partials are visible to the last one without a
+    // release/acquire pair in the source: the partials are stored with sc0
+    // sc1 (system coherence: written through this XCD's L2 to memory, no dirty
+    // line left behind) and read back with sc0 sc1 (past the L2, from the
+    // point of coherence); gfx9 counts stores in vmcnt and returns a
+    // write-through store's count only when the write is acknowledged there,
+    // so vmcnt(0) then the workgroup barrier put every wave's partials in
+    // memory before thread 0's counter add, and the adds themselves are
+    // performed at the point of coherence (system scope), so the slice that
+    // reads KS - 1 comes after every other slice's partials. This is the
+    // sequence the compiler emits for a system-scope release of such stores,
+    // less its L2 write-back (buffer_wbl2), which has nothing to write here,
+    // and its acquire's L2 invalidate, which the sc0 sc1 loads do not need;
+    // both cost microseconds per launch on MI355X. The asm statements carry
+    // memory clobbers, so the compiler keeps every access on its side.
     if (fused) {
         __shared__ unsigned s_last;
         asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // this wave's partials are in memory
@@ -940,7 +936,6 @@ __global__ __launch_bounds__((64 * (CM == 3 ? kChunkWaves<NSRC, MB> : kMaxWavesF
             }
         }
     }
-    ST_TR(6);
 }
 
 // CHK split-K: y[m, n] = epilogue(sum over s < S of part[s][src][m][n]), the
@@ -990,7 +985,7 @@ int launch_kernel(st_context *ctx, Params &p, size_t lds) {
     auto kern = qmv_kernel<FMT, NSRC, XM, MB, SPU, PERM, CM>;
     if (lds > 64 * 1024)
         ST_HIP(hipFuncSetAttribute((const void *)kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds));
-    hipLaunchKernelGGL(kern, dim3(p.grid), dim3(64 * p.nwaves), lds, ctx->stream, p);
+    st::launch(ctx, kern, dim3(p.grid), dim3(64 * p.nwaves), lds, p);
     return launch_check("qmv_kernel");
 }
 
@@ -1060,11 +1055,16 @@ int launch_chk(st_context *ctx, Params &p, bool split, int ncu, int tiles_cu) {
                  !tune(ctx, ST_TUNE_SPLIT_REDUCE_KERNEL, fuse_dflt))
                     ? ctx->split_counters
                     : nullptr;
-        if (int rc = launch_kernel<FMT, NSRC, XM, MB, SPU, PERM, 3>(ctx, p, lds)) return rc;
+        if (int rc = launch_kernel<FMT, NSRC, XM, MB, SPU, PERM, 3>(ctx, p, lds)) {
+            // the counters must be zero for the next call; a launch that did
+            // not go through may not have left them so (an error path, never
+            // inside a capture that is to be replayed)
+            if (p.cnt) (void)hipMemsetAsync(ctx->split_counters, 0, kSplitCounters * sizeof(unsigned), ctx->stream);
+            return rc;
+        }
         if (ks == 1 || p.cnt) return ST_OK;
         const int mn = p.M * p.N;
-        hipLaunchKernelGGL((split_reduce_kernel<NSRC, is_i8(FMT)>), dim3((mn + 255) / 256), dim3(256), 0,
-                           ctx->stream, p.part, p.scale8, p.y, p.M, p.N, ks);
+        st::launch(ctx, (split_reduce_kernel<NSRC, is_i8(FMT)>), dim3((mn + 255) / 256), dim3(256), 0, p.part, p.scale8, p.y, p.M, p.N, ks);
         return launch_check("split_reduce_kernel");
     }
     return -1;

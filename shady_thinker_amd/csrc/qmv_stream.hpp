@@ -41,19 +41,13 @@
 namespace st {
 namespace qmv {
 
-#ifndef ST_STREAM_RING
-#define ST_STREAM_RING 6144
-#endif
-constexpr int kStreamRingPerWave = ST_STREAM_RING;  // LDS ring bytes per wave (D is derived from it)
+constexpr int kStreamRingPerWave = 6144;  // LDS ring bytes per wave (D is derived from it)
 // x staging: at most this many 64-item rows per wave (8-wave workgroups have
 // the registers for three: up to 256 VGPRs a wave)
 template <int NW>
 constexpr int kStreamRows = NW == 8 ? 3 : 2;
 constexpr size_t kLdsBytes = 160 * 1024;
-#ifndef ST_STREAM_PRIO
-#define ST_STREAM_PRIO 1
-#endif
-constexpr bool kStreamPrio = ST_STREAM_PRIO;
+constexpr bool kStreamPrio = true;
 
 template <int FMT, int SPU>
 constexpr int stream_wpu() { return is_i8(FMT) ? 8 : 2 * SPU; }  // weight dwords per lane per unit
@@ -128,7 +122,6 @@ __global__ __launch_bounds__(64 * NW) void qmv_stream_kernel(Params p) {
     const auto range = [&](int w) { return (int)((unsigned)w * (unsigned)U / (unsigned)NW); };
     const int ua = range(wave), ub = range(wave + 1);
     const int nu = ub - ua;
-    ST_TR(0);
 
     const int ASTEP = 4 * RB;                // u32x4 per (group, step) of A
     const int AUNIT = SPU * ASTEP;           // u32x4 per group of A
@@ -226,7 +219,6 @@ __global__ __launch_bounds__(64 * NW) void qmv_stream_kernel(Params p) {
     for (int d = 0; d < D; ++d) issue(d, d);
     if (stager) {
         wait_vm<D * LPU>();  // x has landed; the ring stays in flight
-        ST_TR(1);
 #pragma unroll
         for (int r = 0; r < RMAX; ++r) {
             const int row = wave + r * NW;
@@ -243,10 +235,8 @@ __global__ __launch_bounds__(64 * NW) void qmv_stream_kernel(Params p) {
     }
     if (wave == 0)
         for (int i = lane; i < AUNIT; i += 64) zblk[i] = u32x4{0, 0, 0, 0};
-    ST_TR(2);
     // x staged (and this wave's LDS writes landed) in every wave; the DMAs stay in flight
     asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
-    ST_TR(3);
 
     // -------------------------------------------------------------- compute
     float tot[NSRC];
@@ -393,7 +383,6 @@ __global__ __launch_bounds__(64 * NW) void qmv_stream_kernel(Params p) {
 #pragma unroll
         for (int d = 0; d < D; ++d) {
             if (i0 + d < nu) compute(i0 + d, d);
-            if (i0 + d == 0) ST_TR(7);
             issue(i0 + d + D, d);  // always: the count of loads per unit is fixed
         }
         if (ssync > 0 && ++scount == ssync) {
@@ -410,14 +399,11 @@ __global__ __launch_bounds__(64 * NW) void qmv_stream_kernel(Params p) {
         }
     }
     __builtin_amdgcn_s_setprio(0);
-    ST_TR(4);
     // ------------------------------------------ tiles split across waves
     __syncthreads();
-    ST_TR(5);
     if (nu > 0) {
         const int tl = (ub - 1) / G, ts = tl * G, te = ts + G;
         if (ts >= ua && te > ub) {  // began in this range, continues past it: this wave finishes it
-            ST_TR(10);
             // the first-tile partials of the later waves whose ranges begin
             // inside this tile, added in wave order, without branches (after
             // the barrier the four waves of a SIMD run this part one after
@@ -451,12 +437,9 @@ __global__ __launch_bounds__(64 * NW) void qmv_stream_kernel(Params p) {
                 for (int src = 0; src < NSRC; ++src)
                     v[src] += __builtin_bit_cast(float, __builtin_bit_cast(unsigned, r[k - 1][src]) & keep);
             }
-            ST_TR(8);
             write_y(t0 + tl, v, is_i8(FMT) ? p.scale8[(t0 + tl) * kTileN + c] : 0.0f);
-            ST_TR(9);
         }
     }
-    ST_TR(6);
 }
 
 // One launch shape of the streaming kernel; -1 (nothing launched) when the
@@ -474,7 +457,7 @@ int launch_stream_nw(st_context *ctx, Params &p, int grid) {
     if (!is_i8(FMT) && !p.qz[0] != !p.qz[NSRC - 1]) return -1;  // zero points on one source only
     auto go = [&](auto kern) -> int {
         ST_HIP(hipFuncSetAttribute((const void *)kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)dyn));
-        hipLaunchKernelGGL(kern, dim3(p.grid), dim3(64 * NW), dyn, ctx->stream, p);
+        st::launch(ctx, kern, dim3(p.grid), dim3(64 * NW), dyn, p);
         return launch_check("qmv_stream_kernel");
     };
     if constexpr (!is_i8(FMT)) {

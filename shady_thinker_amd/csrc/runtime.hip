@@ -126,6 +126,11 @@ void *st_context_stream(st_context *ctx) { return ctx ? ctx->stream : nullptr; }
 int st_context_reserve_workspace(st_context *ctx, size_t bytes) {
     if (!ctx) return st::fail(ST_ERR_INVALID, "st_context_reserve_workspace: ctx is NULL");
     if (bytes <= ctx->ws_bytes) return ST_OK;
+    if (ctx->ws_pins > 0)
+        return st::fail(ST_ERR_INVALID,
+                        "st_context_reserve_workspace: %d captured graph(s) point into the workspace; reserve "
+                        "before capturing",
+                        ctx->ws_pins);
     ST_HIP(hipSetDevice(ctx->device));
     ST_HIP(hipStreamSynchronize(ctx->stream));
     float *nws = nullptr;
@@ -147,6 +152,21 @@ int st_context_get_tune(st_context *ctx, int knob, int *value) {
     if (!ctx || !value) return st::fail(ST_ERR_INVALID, "st_context_get_tune: NULL argument");
     if (knob < 0 || knob >= ST_TUNE_COUNT) return st::fail(ST_ERR_INVALID, "st_context_get_tune: knob %d", knob);
     *value = ctx->tune[knob];
+    return ST_OK;
+}
+
+int st_context_set_timing_events(st_context *ctx, void *start, void *stop) {
+    if (!ctx) return st::fail(ST_ERR_INVALID, "st_context_set_timing_events: ctx is NULL");
+    ctx->t_start = static_cast<hipEvent_t>(start);
+    ctx->t_stop = static_cast<hipEvent_t>(stop);
+    return ST_OK;
+}
+
+int st_context_pin_workspace(st_context *ctx, int delta) {
+    if (!ctx) return st::fail(ST_ERR_INVALID, "st_context_pin_workspace: ctx is NULL");
+    if ((delta != 1 && delta != -1) || ctx->ws_pins + delta < 0)
+        return st::fail(ST_ERR_INVALID, "st_context_pin_workspace: delta %d with %d pins held", delta, ctx->ws_pins);
+    ctx->ws_pins += delta;
     return ST_OK;
 }
 

@@ -30,8 +30,8 @@ def _xdtype(t) -> int:
 
 
 def _rows(t, k: int) -> int:
-    if t.numel() % k:
-        raise ValueError(f"input of {t.numel()} elements is not [M, {k}]")
+    if t.numel() % k or t.numel() == 0:
+        raise ValueError(f"input of {t.numel()} elements is not [M, {k}] with M >= 1")
     return t.numel() // k
 
 

@@ -252,6 +252,7 @@ def run_gate_up(gpu, wg, wu, a_np, out_dtype=torch.float32):
     (257, 2048, 520, 256, True, False, True, torch.float16),    # group 256, ragged M
     (64, 4096, 264, 128, False, False, True, torch.float32),    # few tiles: split-K, two launches on one A
     (33, 1024, 1032, 128, "up", False, True, torch.float32),    # zero points on up only
+    (128, 2560, 9728, 128, False, False, True, torch.float16),  # combined grid would not split K, one weight alone would
 ])
 def test_gate_up_gemm_equals_two_gemms(gpu, orc, Mr, K, N, gs, zeros, act, tiled, out):
     """st_gptq_i4_gate_up_gemm: each output bit for bit what st_gptq_i4_gemm

@@ -1,6 +1,7 @@
 """GPU tests of the M-token callers: the fused silu.down prefill GEMM
-(st_gptq_i4_silu_gemm) and DecoderLinears (one layer's projections for
-decode and for prefill), against the f64 oracle through the C ABI."""
+(st_gptq_i4_silu_gemm), DecoderLinears and DeltaNetLinears (one layer's
+projections for decode and for prefill, of either kind), against the f64
+oracle through the C ABI."""
 import numpy as np
 import pytest
 import torch
@@ -145,6 +146,62 @@ def test_decoder_linears_prefill(gpu, orc):
     assert orc.rel_l2(o.float().cpu().numpy(), ref(orc, attn, cs["o"])) < TOL_GEMM
     assert orc.rel_l2(g.float().cpu().numpy(), ref(orc, x, cs["gate"])) < TOL_GEMM
     assert orc.rel_l2(u.float().cpu().numpy(), ref(orc, x, cs["up"])) < TOL_GEMM
+    want_d = ref(orc, orc.silu_gate_f64(g.cpu().numpy(), u.cpu().numpy()), cs["down"])
+    assert orc.rel_l2(d.float().cpu().numpy(), want_d) < TOL_GEMM
+
+
+def _dn_layer(gpu, orc, H, T, Z, I, gs, zeros=False):
+    cs = {}
+    for i, (name, k, n) in enumerate((("in_qkv", H, T), ("in_z", H, Z), ("out", Z, H), ("gate", H, I),
+                                       ("up", H, I), ("down", I, H))):
+        cs[name] = orc.gptq_case(320 + i, k, n, gs, zeros=zeros)
+    ws = {n: up(gpu, c) for n, c in cs.items()}
+    return cs, sta.DeltaNetLinears(ws["in_qkv"], ws["in_z"], ws["out"], ws["gate"], ws["up"], ws["down"])
+
+
+@pytest.mark.parametrize("Mr", [1, 5])
+def test_deltanet_linears_decode(gpu, orc, Mr):
+    """A DeltaNet layer's projections for 1-32 tokens (f32): in_proj_qkv |
+    in_proj_z as one linear, out_proj on silu(z) * core (the reference's
+    fused_silu_gptq_down, src/model.rs:786-791; at several tokens z is
+    copied out of the strided qkv|z rows), the MLP, each against f64."""
+    H, T, Z, I, gs = 256, 384, 128, 512, 128
+    cs, layer = _dn_layer(gpu, orc, H, T, Z, I, gs, zeros=True)
+    rng = np.random.default_rng(40 + Mr)
+    x = rng.standard_normal((Mr, H)).astype(np.float32)
+    core = rng.standard_normal((Mr, Z)).astype(np.float32)
+    qkvz = torch.empty(Mr, T + Z, device="cuda")
+    o, h, d = torch.empty(Mr, H, device="cuda"), torch.empty(Mr, I, device="cuda"), torch.empty(Mr, H, device="cuda")
+    layer.decode(gpu, torch.from_numpy(x).cuda(), torch.from_numpy(core).cuda(), qkvz, o, h, d)
+    torch.cuda.synchronize()
+    y = qkvz.cpu().numpy()
+    assert orc.rel_l2(y[:, :T], ref(orc, x, cs["in_qkv"])) < TOL_DECODE
+    assert orc.rel_l2(y[:, T:], ref(orc, x, cs["in_z"])) < TOL_DECODE
+    # out_proj on the z this call produced
+    assert orc.rel_l2(o.cpu().numpy(), ref(orc, orc.silu_gate_f64(y[:, T:], core), cs["out"])) < TOL_DECODE
+    want_h = orc.silu_gate_f64(ref(orc, x, cs["gate"]), ref(orc, x, cs["up"]))
+    assert orc.rel_l2(h.cpu().numpy(), want_h) < TOL_DECODE
+    assert orc.rel_l2(d.cpu().numpy(), ref(orc, h.cpu().numpy(), cs["down"])) < TOL_DECODE
+
+
+def test_deltanet_linears_prefill(gpu, orc):
+    """The same for a 40-token block (f16) through the GEMM: out_proj is
+    st_gptq_i4_silu_gemm on z and the core's output."""
+    H, T, Z, I, gs, Mr = 256, 384, 128, 512, 128, 40
+    cs, layer = _dn_layer(gpu, orc, H, T, Z, I, gs)
+    rng = np.random.default_rng(9)
+    x = rng.standard_normal((Mr, H)).astype(np.float16)
+    core = rng.standard_normal((Mr, Z)).astype(np.float16)
+    f16 = dict(device="cuda", dtype=torch.float16)
+    qkvz, o = torch.empty(Mr, T + Z, **f16), torch.empty(Mr, H, **f16)
+    g, u, d = torch.empty(Mr, I, **f16), torch.empty(Mr, I, **f16), torch.empty(Mr, H, **f16)
+    layer.prefill(gpu, torch.from_numpy(x).cuda(), torch.from_numpy(core).cuda(), qkvz, o, g, u, d)
+    torch.cuda.synchronize()
+    y = qkvz.float().cpu().numpy()
+    assert orc.rel_l2(y[:, :T], ref(orc, x, cs["in_qkv"])) < TOL_GEMM
+    assert orc.rel_l2(y[:, T:], ref(orc, x, cs["in_z"])) < TOL_GEMM
+    want_o = ref(orc, orc.silu_gate_f64(qkvz[:, T:].cpu().numpy(), core), cs["out"])
+    assert orc.rel_l2(o.float().cpu().numpy(), want_o) < TOL_GEMM
     want_d = ref(orc, orc.silu_gate_f64(g.cpu().numpy(), u.cpu().numpy()), cs["down"])
     assert orc.rel_l2(d.float().cpu().numpy(), want_d) < TOL_GEMM
 

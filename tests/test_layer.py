@@ -55,3 +55,53 @@ def test_decode_token_limit():
     layer = sta.DecoderLinears(**parts())
     with pytest.raises(ValueError):
         layer.decode(None, torch.zeros(33, 256), torch.zeros(33, 256), None, None, None, None)
+
+
+def dn_parts(H=256, T=384, Z=128, I=512):
+    return dict(in_qkv=w(H, T), in_z=w(H, Z), out=w(Z, H), gate=w(H, I), up=w(H, I), down=w(I, H))
+
+
+def test_deltanet_construction_concatenates_qkv_and_z():
+    p = dn_parts()
+    layer = sta.DeltaNetLinears(**p)
+    assert layer.kind == "linear_attn" and layer.qkv.N == 384 + 128 and layer.splits == (384, 128)
+    assert (layer.hidden, layer.attn_dim, layer.inter) == (256, 128, 512)
+    y = torch.zeros(3, layer.qkv.N)
+    assert layer.z_of(y).shape == (3, 128)
+
+
+@pytest.mark.parametrize("bad,shape", [("out", (256, 256)), ("out", (128, 64)), ("in_z", (128, 128)),
+                                       ("down", (256, 256))])
+def test_deltanet_inconsistent_shapes_are_rejected(bad, shape):
+    p = dn_parts()
+    p[bad] = w(*shape)
+    with pytest.raises(ValueError):
+        sta.DeltaNetLinears(**p)
+
+
+def test_layer_kind_by_reference_names():
+    """The reference's loader takes a layer as self-attention when its
+    self_attn.q_proj is present (src/weights.rs:247-250), else as DeltaNet
+    with linear_attn.{in_proj_qkv,in_proj_z,out_proj} (:478-483)."""
+    sa, dn = parts(), dn_parts()
+    names = {"q": "self_attn.q_proj", "k": "self_attn.k_proj", "v": "self_attn.v_proj", "o": "self_attn.o_proj",
+             "gate": "mlp.gate_proj", "up": "mlp.up_proj", "down": "mlp.down_proj"}
+    dnames = {"in_qkv": "linear_attn.in_proj_qkv", "in_z": "linear_attn.in_proj_z", "out": "linear_attn.out_proj",
+              "gate": "mlp.gate_proj", "up": "mlp.up_proj", "down": "mlp.down_proj"}
+    linears = {f"model.layers.0.{dnames[n]}": x for n, x in dn.items()}
+    linears.update({f"model.layers.1.{names[n]}": x for n, x in sa.items()})
+    L0 = sta.layer_from_linears(linears, 0)
+    L1 = sta.layer_from_linears(linears, 1)
+    assert L0.kind == "linear_attn" and L0.o is dn["out"] and L0.down is dn["down"]
+    assert L1.kind == "self_attn" and L1.o is sa["o"]
+    with pytest.raises(KeyError):
+        sta.DeltaNetLinears.from_linears(linears, 1)
+    with pytest.raises(KeyError):
+        sta.layer_from_linears(linears, 2)
+    st = sta.DecoderStack.from_linears(linears, 2, w(256, 1000))
+    assert [L.kind for L in st.layers] == ["linear_attn", "self_attn"] and st.vocab == 1000
+
+
+def test_stack_rejects_mixed_hidden_sizes():
+    with pytest.raises(ValueError):
+        sta.DecoderStack([sta.DecoderLinears(**parts()), sta.DeltaNetLinears(**dn_parts(I=256))], w(256, 64))

@@ -60,6 +60,8 @@ def test_valid_arguments_reach_the_c_abi():
     (dict(perm=torch.zeros(K - 1, dtype=torch.int32)), ValueError),
     (dict(x=torch.zeros(1, K, dtype=torch.bfloat16)), TypeError),
     (dict(x=torch.zeros(K, 2)[:, 0].reshape(1, K)), ValueError),   # non-contiguous input
+    (dict(x=torch.zeros(K + 8)), ValueError),                        # not a whole number of rows
+    (dict(x=torch.zeros(0, K)), ValueError),                         # no rows
 ])
 def test_matvec_rejects(kw, exc):
     with pytest.raises(exc):
