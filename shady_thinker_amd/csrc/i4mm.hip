@@ -7,9 +7,10 @@
 //
 //  * Exact products: (q - z) is an integer in [-15, 15], exact in f16 (the
 //    f16 1024 bias: 1024 + q, minus 1024 + z). f16 x is used as is. f32 x is
-//    split once, by a pre-pass into the context workspace, per token and per
-//    128 k: x 2^-e (2^e just above the block's largest |x|) = hi + lo, two
-//    f16 rows of the MFMA A operand (about 22 significant bits). Every
+//    split per token and per 128 k: x 2^-e (2^e just above the block's
+//    largest |x|) = hi + lo, two f16 rows of the MFMA A operand (about 22
+//    significant bits), as each chunk of x is staged into LDS (with
+//    act-order, by a pre-pass into the context workspace). Every
 //    product is exact in f32; each 64 (or 128) k block sums into a fresh
 //    accumulator that is then scaled by s 2^e in f32.
 //  * Every weight is read from HBM once for all tokens (the integer-limb
@@ -150,7 +151,8 @@ __global__ __launch_bounds__(256) void i4mm_prep_kernel(const float *__restrict_
     if (l == 0) pe[(size_t)t * units + u] = __builtin_amdgcn_ldexpf(1.0f, ex);
 }
 
-// F32X: x is the pre-pass output (xp, pe: two f16 rows per token) or f16 x;
+// XM: f16 x (0), the pre-pass output (1: xp, pe, two f16 rows per token) or
+// f32 x split at staging (2);
 // NSRC: 1 (matvec) or 2 (gate/up); MB: 16-row MFMA blocks; KCU: 128-k units
 // per staged chunk; GW: units per wave per chunk (S = KCU / GW waves per tile
 // and source).
@@ -159,13 +161,18 @@ __global__ __launch_bounds__(256) void i4mm_prep_kernel(const float *__restrict_
 // PAIR (two sources): a wave takes its units of both the gate and the up
 // weight of a tile, so every x fragment read from LDS and every load
 // address serves two MFMA chains.
-template <bool F32X, int NSRC, int MB, int GS, int KCU, int GW, int NW, bool PAIR>
+template <int XM, int NSRC, int MB, int GS, int KCU, int GW, int NW, bool PAIR>
 __global__ __launch_bounds__(64 * NW) void i4mm_kernel(const void *__restrict__ x, const float *__restrict__ pe,
                                                         const uint32_t *__restrict__ qw0,
                                                         const uint16_t *__restrict__ sc0, const uint32_t *__restrict__ qz0,
                                                         const uint32_t *__restrict__ qw1, const uint16_t *__restrict__ sc1,
                                                         const uint32_t *__restrict__ qz1, int zoff, float *__restrict__ y,
                                                         int M, int K, int N, int ntiles) {
+    // XM: 0 f16 x; 1 f32 x split by i4mm_prep_kernel (hi / lo rows and
+    // factors in the workspace); 2 f32 x split here, at staging, with the
+    // same arithmetic (no pre-pass launch)
+    constexpr bool F32X = XM != 0;
+    constexpr bool RAW = XM == 2;
     constexpr int kKC = 128 * KCU;        // k per staged chunk
     constexpr int kPitch = kKC + 8;       // halves per LDS row (16-byte pad: fragment rows on distinct banks)
     constexpr int S = KCU / GW;
@@ -179,6 +186,11 @@ __global__ __launch_bounds__(64 * NW) void i4mm_kernel(const void *__restrict__ 
     constexpr int XITEMS = ROWS * (kKC / 8);
     constexpr int kThr = 64 * NW;
     constexpr int XL = (XITEMS + kThr - 1) / kThr;
+    // RAW: items of 8 k of one token (32 bytes of f32 x, two loads), each
+    // giving the 8 k of its hi and lo rows; 16 consecutive items (lanes of
+    // one DPP row) are one 128-k unit of one token
+    constexpr int RITEMS = (ROWS / 2) * (kKC / 8);
+    constexpr int XLR = (RITEMS + kThr - 1) / kThr;
     // two x buffers; at the end, the partial sums of every wave
     constexpr int PS = PAIR ? 2 : 1;  // sources per wave
     static_assert(!PAIR || NSRC == 2, "PAIR needs two sources");
@@ -228,9 +240,21 @@ __global__ __launch_bounds__(64 * NW) void i4mm_kernel(const void *__restrict__ 
     // Rows already in B order: the chunk is copied. With f32 x, threads
     // tid < KCU 16 also copy the chunk's 2^e factors (unit tid / 16, token tid % 16).
     const int nrows = F32X ? 2 * M : M;
-    u32x4 xr2[1][XL];  // the next chunk of x
+    u32x4 xr2[1][RAW ? 2 * XLR : XL];  // the next chunk of x
     unsigned pr2[1];
-    auto load_x = [&](u32x4 (&xr)[XL], unsigned &pr, int c) {
+    auto load_x = [&](u32x4 (&xr)[RAW ? 2 * XLR : XL], unsigned &pr, int c) {
+        if constexpr (RAW) {
+#pragma unroll
+            for (int j = 0; j < XLR; ++j) {
+                const int i = j * kThr + tid;
+                const int t = i / (kKC / 8), k = c * kKC + 8 * (i % (kKC / 8));
+                const bool ok = i < RITEMS && t < M && k < K;
+                const unsigned o = ok ? (unsigned)(t * K + k) * 4u : kNoLoad;
+                xr[2 * j] = __builtin_amdgcn_raw_buffer_load_b128(rx, o, 0, 0);
+                xr[2 * j + 1] = __builtin_amdgcn_raw_buffer_load_b128(rx, ok ? o + 16u : kNoLoad, 0, 0);
+            }
+            return;
+        }
 #pragma unroll
         for (int j = 0; j < XL; ++j) {
             const int i = j * kThr + tid;
@@ -244,7 +268,45 @@ __global__ __launch_bounds__(64 * NW) void i4mm_kernel(const void *__restrict__ 
             pr = __builtin_amdgcn_raw_buffer_load_b32(rp, ok ? (unsigned)(t * units + u) * 4u : kNoLoad, 0, 0);
         }
     };
-    auto store_x = [&](const u32x4 (&xr)[XL], unsigned pr, _Float16 *xs, float *ps) {
+    auto store_x = [&](const u32x4 (&xr)[RAW ? 2 * XLR : XL], unsigned pr, _Float16 *xs, float *ps) {
+        if constexpr (RAW) {
+            // the split of i4mm_prep_kernel: x 2^-e (2^e just above the
+            // unit's largest |x|) = hi + lo, 8 k per item in B order
+#pragma unroll
+            for (int j = 0; j < XLR; ++j) {
+                const int i = j * kThr + tid;
+                // (each word through a scalar first: hipcc's __builtin_bit_cast
+                // of an ext_vector component reads component 0)
+                const u32x4 a = xr[2 * j], b = xr[2 * j + 1];
+                const unsigned wv[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+                float v[8];
+#pragma unroll
+                for (int e = 0; e < 8; ++e) v[e] = __uint_as_float(wv[e]);
+                float amax = 0.f;
+#pragma unroll
+                for (int e = 0; e < 8; ++e) amax = fmaxf(amax, fabsf(v[e]));
+                amax = row_max(amax);  // every lane takes part (items past the end read zeros)
+                const int ex = amax > 0.f ? __builtin_amdgcn_frexp_expf(amax) : 0;
+                const float down = __builtin_amdgcn_ldexpf(1.0f, -ex);
+                unsigned hw[4], lw[4];
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    const float x0 = v[2 * e] * down, x1 = v[2 * e + 1] * down;
+                    const _Float16 h0 = (_Float16)x0, h1 = (_Float16)x1;
+                    const _Float16 l0 = (_Float16)(x0 - (float)h0), l1 = (_Float16)(x1 - (float)h1);
+                    hw[e] = (unsigned)__builtin_bit_cast(uint16_t, h0) | ((unsigned)__builtin_bit_cast(uint16_t, h1) << 16);
+                    lw[e] = (unsigned)__builtin_bit_cast(uint16_t, l0) | ((unsigned)__builtin_bit_cast(uint16_t, l1) << 16);
+                }
+                const u32x4 H = {hw[0], hw[1], hw[2], hw[3]}, L = {lw[0], lw[1], lw[2], lw[3]};
+                if (RITEMS % kThr == 0 || i < RITEMS) {
+                    const int t = i / (kKC / 8), kq = i % (kKC / 8);
+                    *reinterpret_cast<u32x4 *>(&xs[(2 * t) * kPitch + 8 * kq]) = to_b_order(H);
+                    *reinterpret_cast<u32x4 *>(&xs[(2 * t + 1) * kPitch + 8 * kq]) = to_b_order(L);
+                    if ((kq & 15) == 0) ps[(kq >> 4) * 16 + t] = __builtin_amdgcn_ldexpf(1.0f, ex);
+                }
+            }
+            return;
+        }
 #pragma unroll
         for (int j = 0; j < XL; ++j) {
             const int i = j * kThr + tid;
@@ -428,13 +490,13 @@ __global__ __launch_bounds__(64 * NW) void i4mm_kernel(const void *__restrict__ 
         }
 }
 
-template <bool F32X, int NSRC, int MB, int GS>
+template <int XM, int NSRC, int MB, int GS>
 int launch_gs(st_context *ctx, const void *x, const float *pe, const uint32_t *const *qw, const uint16_t *const *sc,
               const uint32_t *const *qz, int zoff, float *y, int M, int K, int N, int ntiles, int G, int wpt, int nw,
               bool pair) {
     const dim3 grid(G);
 #define ST_I4MM_P(KCU_, GW_, NW_, PAIR_)                                                                          \
-    st::launch(ctx, (i4mm_kernel<F32X, NSRC, MB, GS, KCU_, GW_, NW_, PAIR_>), grid, dim3(64 * NW_), 0, x, \
+    st::launch(ctx, (i4mm_kernel<XM, NSRC, MB, GS, KCU_, GW_, NW_, PAIR_>), grid, dim3(64 * NW_), 0, x, \
                        pe, qw[0], sc[0], qz[0], qw[1], sc[1], qz[1], zoff, y, M, K, N, ntiles)
 #define ST_I4MM(KCU_, GW_, NW_) ST_I4MM_P(KCU_, GW_, NW_, false)
     // gate/up with both sources in a wave: wpt is then waves per tile pair
@@ -487,27 +549,27 @@ __global__ __launch_bounds__(256) void i4mm_gather_kernel(const uint16_t *__rest
     *reinterpret_cast<u32x4 *>(xg + i) = v;
 }
 
-template <bool F32X, int NSRC, int MB>
+template <int XM, int NSRC, int MB>
 int launch_mb(st_context *ctx, const void *x, const float *pe, const uint32_t *const *qw, const uint16_t *const *sc,
               const uint32_t *const *qz, int zoff, float *y, int M, int K, int N, int gs, int ntiles, int G, int wpt,
               int nw, bool pair) {
     switch (gs) {
-        case 64: return launch_gs<F32X, NSRC, MB, 64>(ctx, x, pe, qw, sc, qz, zoff, y, M, K, N, ntiles, G, wpt, nw, pair);
+        case 64: return launch_gs<XM, NSRC, MB, 64>(ctx, x, pe, qw, sc, qz, zoff, y, M, K, N, ntiles, G, wpt, nw, pair);
         case 128:
-            return launch_gs<F32X, NSRC, MB, 128>(ctx, x, pe, qw, sc, qz, zoff, y, M, K, N, ntiles, G, wpt, nw, pair);
+            return launch_gs<XM, NSRC, MB, 128>(ctx, x, pe, qw, sc, qz, zoff, y, M, K, N, ntiles, G, wpt, nw, pair);
         default:
-            return launch_gs<F32X, NSRC, MB, 256>(ctx, x, pe, qw, sc, qz, zoff, y, M, K, N, ntiles, G, wpt, nw, pair);
+            return launch_gs<XM, NSRC, MB, 256>(ctx, x, pe, qw, sc, qz, zoff, y, M, K, N, ntiles, G, wpt, nw, pair);
     }
 }
 
-template <bool F32X, int NSRC>
+template <int XM, int NSRC>
 int launch_src(st_context *ctx, const void *x, const float *pe, const uint32_t *const *qw, const uint16_t *const *sc,
                const uint32_t *const *qz, int zoff, float *y, int M, int K, int N, int gs, int ntiles, int G, int wpt,
                int nw, bool pair) {
     // tokens per 16-row block: 8 (f32 x: hi and lo rows) or 16
-    const int mb = (M * (F32X ? 2 : 1) + 15) / 16;
-    return mb <= 1 ? launch_mb<F32X, NSRC, 1>(ctx, x, pe, qw, sc, qz, zoff, y, M, K, N, gs, ntiles, G, wpt, nw, pair)
-                   : launch_mb<F32X, NSRC, 2>(ctx, x, pe, qw, sc, qz, zoff, y, M, K, N, gs, ntiles, G, wpt, nw, pair);
+    const int mb = (M * (XM ? 2 : 1) + 15) / 16;
+    return mb <= 1 ? launch_mb<XM, NSRC, 1>(ctx, x, pe, qw, sc, qz, zoff, y, M, K, N, gs, ntiles, G, wpt, nw, pair)
+                   : launch_mb<XM, NSRC, 2>(ctx, x, pe, qw, sc, qz, zoff, y, M, K, N, gs, ntiles, G, wpt, nw, pair);
 }
 
 }  // namespace
@@ -546,7 +608,10 @@ int int4_mm_f16(st_context *ctx, const void *x, bool x_f32, const int32_t *perm,
     }
     const void *xa = x;
     const float *pe = nullptr;
-    if (x_f32) {  // the pre-pass writes [2M, K] f16 rows and [M, K / 128] factors into the workspace
+    // f32 x without act-order: split inside the kernel (XM 2); with
+    // act-order, or when the setting asks for it, by the pre-pass (XM 1)
+    const bool split_in = x_f32 && !perm && tune(ctx, ST_TUNE_I4MM_PREPASS, 0) != 1;
+    if (x_f32 && !split_in) {  // the pre-pass writes [2M, K] f16 rows and [M, K / 128] factors into the workspace
         const size_t xbytes = ((size_t)2 * M * K * 2 + 255) & ~size_t(255);
         if (!ctx->ws || xbytes + (size_t)M * (K / 128) * 4 > ctx->ws_bytes)
             return fail(ST_ERR_WORKSPACE, "int4_mm_f16: workspace below %zu B", xbytes + (size_t)M * (K / 128) * 4);
@@ -565,11 +630,14 @@ int int4_mm_f16(st_context *ctx, const void *x, bool x_f32, const int32_t *perm,
         if (int rc = launch_check("i4mm_gather_kernel")) return rc;
         xa = xg;
     }
+    if (split_in)
+        return nsrc == 2 ? launch_src<2, 2>(ctx, xa, pe, qw, sc, qz, zoff, y, M, K, N, gs, ntiles, G, wpt, nw, pair)
+                         : launch_src<2, 1>(ctx, xa, pe, qw, sc, qz, zoff, y, M, K, N, gs, ntiles, G, wpt, nw, pair);
     if (nsrc == 2)
-        return x_f32 ? launch_src<true, 2>(ctx, xa, pe, qw, sc, qz, zoff, y, M, K, N, gs, ntiles, G, wpt, nw, pair)
-                     : launch_src<false, 2>(ctx, xa, pe, qw, sc, qz, zoff, y, M, K, N, gs, ntiles, G, wpt, nw, pair);
-    return x_f32 ? launch_src<true, 1>(ctx, xa, pe, qw, sc, qz, zoff, y, M, K, N, gs, ntiles, G, wpt, nw, pair)
-                 : launch_src<false, 1>(ctx, xa, pe, qw, sc, qz, zoff, y, M, K, N, gs, ntiles, G, wpt, nw, pair);
+        return x_f32 ? launch_src<1, 2>(ctx, xa, pe, qw, sc, qz, zoff, y, M, K, N, gs, ntiles, G, wpt, nw, pair)
+                     : launch_src<0, 2>(ctx, xa, pe, qw, sc, qz, zoff, y, M, K, N, gs, ntiles, G, wpt, nw, pair);
+    return x_f32 ? launch_src<1, 1>(ctx, xa, pe, qw, sc, qz, zoff, y, M, K, N, gs, ntiles, G, wpt, nw, pair)
+                 : launch_src<0, 1>(ctx, xa, pe, qw, sc, qz, zoff, y, M, K, N, gs, ntiles, G, wpt, nw, pair);
 }
 
 }  // namespace st

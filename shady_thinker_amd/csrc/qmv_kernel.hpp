@@ -1048,8 +1048,10 @@ int launch_chk(st_context *ctx, Params &p, bool split, int ncu, int tiles_cu) {
         // tokens 9.8 -> 8.9 us, Llama-7B down 11.9 -> 10.9, o and down at
         // 8 tokens 0.3-0.8 us faster; at 16 tokens the last slice's
         // reads (4 token blocks) cost more than the reduce launch
-        // (0.2-0.6 us slower). Not when the context has no counters or
-        // the setting asks for the reduce kernel.
+        // (0.2-0.6 us slower per call; the configs[4] stack at 16 tokens
+        // 1950 us per step with the reduce launch, 2048 fused). Not when
+        // the context has no counters or the setting asks for the reduce
+        // kernel.
         const int fuse_dflt = MB <= 2 ? 0 : 1;
         p.cnt = (ks > 1 && ctx->split_counters && grid <= kSplitCounters &&
                  !tune(ctx, ST_TUNE_SPLIT_REDUCE_KERNEL, fuse_dflt))

@@ -862,6 +862,45 @@ def test_int4_mm_f16(gpu, orc, Mr, K, N, gs, zeros, f16, dual, tune):
     assert orc.rel_l2(run(), ref) < TOL
 
 
+@pytest.mark.parametrize("Mr,K,N,gs,zeros,dual", [
+    (2, 128, 64, 128, False, False),       # one unit, one tile
+    (5, 384, 72, 64, True, False),         # group 64, ragged last tile
+    (16, 2560, 6144, 128, False, False),   # configs[4] q|k|v at batch 16
+    (9, 4096, 520, 256, True, False),      # group 256, two 16-row blocks
+    (3, 256, 36880, 128, False, False),    # more workgroups than CUs
+    (16, 2560, 9728, 128, False, True),    # configs[4] gate/up at batch 16
+    (6, 1536, 776, 64, True, True),        # gate/up, zeros, group 64
+])
+def test_int4_mm_f16_split_in_kernel(gpu, orc, Mr, K, N, gs, zeros, dual, tune):
+    """f32 x on the f16-MFMA kernel is split into its hi / lo f16 rows and
+    per-unit power-of-two factors inside the kernel, at staging (no
+    pre-pass launch): the same arithmetic as the pre-pass, so y equals the
+    pre-pass path (I4MM_PREPASS=1) bit for bit, and the f64 oracle within
+    1e-5. x spans large and tiny magnitudes (per-unit exponents differ)."""
+    _force_i4mm(tune)
+    c = orc.gptq_case(330 + Mr, K, N, gs, zeros=zeros, M=Mr)
+    x = c["x"].copy()
+    x[:, : K // 2] *= np.float32(3e4)
+    x[:, K // 2:] *= np.float32(1e-3)
+    x[0, :128] = 0.0  # an all-zero unit: factor 1
+    w = up(gpu, c)
+    ref = orc.gptq_matvec_f64(x, c["qweight"], c["scales"], K, N, gs, qzeros=c["qzeros"])
+    if dual:
+        c2 = orc.gptq_case(340 + Mr, K, N, gs, zeros=zeros)
+        w2 = up(gpu, c2)
+        ref = orc.silu_gate_f64(ref, orc.gptq_matvec_f64(x, c2["qweight"], c2["scales"], K, N, gs, qzeros=c2["qzeros"]))
+        run = lambda: _gate_up(gpu, w, w2, x)
+    else:
+        run = lambda: run_matvec(gpu, w, x, torch.float32)
+    y_in = run()
+    tune(I4MM_PREPASS=1)
+    y_pre = run()
+    np.testing.assert_array_equal(y_in, y_pre)
+    e = orc.rel_l2(y_in, ref)
+    print(f"int4 f16-MFMA in-kernel split M={Mr} K={K} N={N} gs={gs} dual={dual} rel-L2 {e:.3e}")
+    assert np.isfinite(y_in).all() and e < 1e-5
+
+
 @pytest.mark.parametrize("Mr,K,N,gs,zeros,f16,dual", [
     (16, 2560, 9728, 128, False, False, True),   # configs[4] gate/up: 608 tile pairs, 3 per workgroup
     (9, 1024, 11008, 128, True, True, True),     # Llama-7B gate/up width, f16 x, zeros
