@@ -87,10 +87,13 @@ inline int launch_check(const char *what) {
 // with the kernel's own start and end (the dispatch's timestamps, as a
 // profiler sees them, without the gap between launches): t_start on the first
 // launch after arming, t_stop on every launch, so that over a call of several
-// launches the pair spans all of them.
+// launches the pair spans all of them. A stream under capture gets plain
+// launches (the events are left alone).
 template <typename F, typename... Args>
 inline void launch(st_context *ctx, F kernel, dim3 grid, dim3 block, size_t lds, Args... args) {
-    if (ctx->t_start || ctx->t_stop) {
+    hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+    if ((ctx->t_start || ctx->t_stop) && hipStreamIsCapturing(ctx->stream, &cs) == hipSuccess &&
+        cs == hipStreamCaptureStatusNone) {
         hipExtLaunchKernelGGL(kernel, grid, block, (std::uint32_t)lds, ctx->stream, ctx->t_start, ctx->t_stop, 0u,
                               args...);
         ctx->t_start = nullptr;

@@ -152,3 +152,21 @@ def test_stack_checks(gpu, stack):
     bad = torch.zeros(V, H + 8, dtype=torch.int16, device="cuda")
     with pytest.raises(ValueError):
         sta.DecoderStack(st.layers, bad)
+
+
+def test_captured_stack_pins_the_workspace(gpu, stack):
+    """A captured step holds pointers into the context workspace: while its
+    StackGraph lives, growing the workspace is refused; after release() it
+    is allowed again."""
+    st, _, _ = stack
+    b = st.buffers(gpu, 16)
+    g = st.capture(gpu, b)
+    big = 1 << 28
+    with pytest.raises(sta.ShadyHipError):
+        gpu.reserve_workspace(big)
+    g.replay()
+    torch.cuda.synchronize()
+    g.release()
+    gpu.reserve_workspace(big)
+    with pytest.raises(RuntimeError):
+        g.replay()
