@@ -161,7 +161,8 @@ __global__ __launch_bounds__(256) void i4mm_prep_kernel(const float *__restrict_
 // PAIR (two sources): a wave takes its units of both the gate and the up
 // weight of a tile, so every x fragment read from LDS and every load
 // address serves two MFMA chains.
-template <int XM, int NSRC, int MB, int GS, int KCU, int GW, int NW, bool PAIR>
+// HZ: some source has zero points (without, no zero words are loaded: z = 8).
+template <int XM, int NSRC, int MB, int GS, int KCU, int GW, int NW, bool PAIR, bool HZ>
 __global__ __launch_bounds__(64 * NW) void i4mm_kernel(const void *__restrict__ x, const float *__restrict__ pe,
                                                         const uint32_t *__restrict__ qw0,
                                                         const uint16_t *__restrict__ sc0, const uint32_t *__restrict__ qz0,
@@ -240,8 +241,9 @@ __global__ __launch_bounds__(64 * NW) void i4mm_kernel(const void *__restrict__ 
     // Rows already in B order: the chunk is copied. With f32 x, threads
     // tid < KCU 16 also copy the chunk's 2^e factors (unit tid / 16, token tid % 16).
     const int nrows = F32X ? 2 * M : M;
-    u32x4 xr2[1][RAW ? 2 * XLR : XL];  // the next chunk of x
-    unsigned pr2[1];
+    constexpr int XS = NW <= 12 ? 2 : 1;
+    u32x4 xr2[XS][RAW ? 2 * XLR : XL];
+    unsigned pr2[XS];
     auto load_x = [&](u32x4 (&xr)[RAW ? 2 * XLR : XL], unsigned &pr, int c) {
         if constexpr (RAW) {
 #pragma unroll
@@ -332,23 +334,39 @@ __global__ __launch_bounds__(64 * NW) void i4mm_kernel(const void *__restrict__ 
             const int u = c * KCU + slice * GW + gi;
             const bool ok = active && u < units;
             if constexpr (GS == 64) {
-                const unsigned o0 = ok ? (unsigned)(((T * G + 2 * u) * 64 + lane) * 8) : kNoLoad;
+                unsigned o0 = ok ? (unsigned)(((T * G + 2 * u) * 64 + lane) * 8) : kNoLoad;
+                asm volatile("" : "+v"(o0));
                 const u32x2 a = __builtin_amdgcn_raw_buffer_load_b64(rw[ps], o0, 0, 0);
                 const u32x2 b = __builtin_amdgcn_raw_buffer_load_b64(rw[ps], o0, 64 * 8, 0);
                 du.w = u32x4{a.x, a.y, b.x, b.y};
-            } else if constexpr (GS == 128) {
-                du.w = __builtin_amdgcn_raw_buffer_load_b128(
-                    rw[ps], ok ? (unsigned)(((T * G + u) * 64 + lane) * 16) : kNoLoad, 0, 0);
             } else {
-                du.w = __builtin_amdgcn_raw_buffer_load_b128(
-                    rw[ps], ok ? (unsigned)(((T * G + u / 2) * 64 + lane) * 32 + 16 * (u & 1)) : kNoLoad, 0, 0);
+                // (offsets pinned in VGPRs: see the scale loads below)
+                unsigned ow = ok ? (GS == 128 ? (unsigned)(((T * G + u) * 64 + lane) * 16)
+                                              : (unsigned)(((T * G + u / 2) * 64 + lane) * 32 + 16 * (u & 1)))
+                                 : kNoLoad;
+                asm volatile("" : "+v"(ow));
+                du.w = __builtin_amdgcn_raw_buffer_load_b128(rw[ps], ow, 0, 0);
             }
 #pragma unroll
             for (int j = 0; j < NG; ++j) {
                 const int g = GS == 64 ? 2 * u + j : (u * 128) / GS;
-                du.s[j] = __builtin_amdgcn_raw_buffer_load_b16(rs[ps], ok ? (unsigned)(g * N + n) * 2u : kNoLoad, 0, 0);
-                du.z[j] = __builtin_amdgcn_raw_buffer_load_b32(
-                    rz[ps], (ok && has_z[ps]) ? (unsigned)(g * (N / 8) + n / 8) * 4u : kNoLoad, 0, 0);
+                // offsets pinned in VGPRs: left as selects on a uniform
+                // condition, the compiler turned each load into two loads on
+                // two branches, and its load waits after those joins drained
+                // the loads of the chunks in flight
+                // (with zero words in the stream the compiler's waits before
+                // a chunk's compute still drain the previous chunk's loads:
+                // symmetric weights, the common case, load none)
+                unsigned os = ok ? (unsigned)(g * N + n) * 2u : kNoLoad;
+                asm volatile("" : "+v"(os));
+                du.s[j] = __builtin_amdgcn_raw_buffer_load_b16(rs[ps], os, 0, 0);
+                if constexpr (HZ) {
+                    unsigned oz = (ok && has_z[ps]) ? (unsigned)(g * (N / 8) + n / 8) * 4u : kNoLoad;
+                    asm volatile("" : "+v"(oz));
+                    du.z[j] = __builtin_amdgcn_raw_buffer_load_b32(rz[ps], oz, 0, 0);
+                } else {
+                    du.z[j] = 0;
+                }
             }
         }
     };
@@ -386,7 +404,7 @@ __global__ __launch_bounds__(64 * NW) void i4mm_kernel(const void *__restrict__ 
                 f32x4 acc[PS][MB];
 #pragma unroll
                 for (int ps = 0; ps < PS; ++ps) {
-                    const int z = has_z[ps] ? (int)((src_u[gi][ps].z[j] >> (4 * (n & 7))) & 0xF) + zoff : 8;
+                    const int z = (HZ && has_z[ps]) ? (int)((src_u[gi][ps].z[j] >> (4 * (n & 7))) & 0xF) + zoff : 8;
                     const _Float16 zl = (_Float16)(1024 + z), zh = (_Float16)(-(64 + z));
                     zlo[ps] = half2_t{zl, zl};
                     zhi[ps] = half2_t{zh, zh};
@@ -432,16 +450,20 @@ __global__ __launch_bounds__(64 * NW) void i4mm_kernel(const void *__restrict__ 
     // index is compile-time; loads are unconditional (past the end they read
     // nothing), so the compiler's wait counts are the same on every path.
     load_x(xr2[0], pr2[0], 0);
+    if constexpr (XS == 2) load_x(xr2[1], pr2[1], 1);
     load_u(ur[0], 0);
     load_u(ur[1], 1);
     store_x(xr2[0], pr2[0], xs0, ps0);
     lds_barrier();
     auto chunk = [&](auto P, int c) {
         constexpr int p = decltype(P)::value;
-        load_x(xr2[0], pr2[0], c + 1);
+        load_x(xr2[p % XS], pr2[p % XS], c + XS);
         load_u(ur[(p + 2) % 3], c + 2);
+        // the chunk's loads stay at its top (left alone, the scheduler sank
+        // some into the compute below, where their issue then waited)
+        __builtin_amdgcn_sched_barrier(0);
         compute(p % 2 ? xs1 : xs0, p % 2 ? ps1 : ps0, ur[p % 3]);
-        store_x(xr2[0], pr2[0], p % 2 ? xs0 : xs1, p % 2 ? ps0 : ps1);  // chunk c + 1
+        store_x(xr2[(p + 1) % XS], pr2[(p + 1) % XS], p % 2 ? xs0 : xs1, p % 2 ? ps0 : ps1);  // chunk c + 1
         lds_barrier();
     };
     for (int c = 0; c < nch; c += 6) {
@@ -495,9 +517,16 @@ int launch_gs(st_context *ctx, const void *x, const float *pe, const uint32_t *c
               const uint32_t *const *qz, int zoff, float *y, int M, int K, int N, int ntiles, int G, int wpt, int nw,
               bool pair) {
     const dim3 grid(G);
-#define ST_I4MM_P(KCU_, GW_, NW_, PAIR_)                                                                          \
-    st::launch(ctx, (i4mm_kernel<XM, NSRC, MB, GS, KCU_, GW_, NW_, PAIR_>), grid, dim3(64 * NW_), 0, x, \
-                       pe, qw[0], sc[0], qz[0], qw[1], sc[1], qz[1], zoff, y, M, K, N, ntiles)
+    const bool hz = qz[0] || (NSRC == 2 && qz[1]);
+#define ST_I4MM_P(KCU_, GW_, NW_, PAIR_)                                                                           \
+    do {                                                                                                           \
+        if (hz)                                                                                                    \
+            st::launch(ctx, (i4mm_kernel<XM, NSRC, MB, GS, KCU_, GW_, NW_, PAIR_, true>), grid, dim3(64 * NW_), 0,  \
+                       x, pe, qw[0], sc[0], qz[0], qw[1], sc[1], qz[1], zoff, y, M, K, N, ntiles);                \
+        else                                                                                                       \
+            st::launch(ctx, (i4mm_kernel<XM, NSRC, MB, GS, KCU_, GW_, NW_, PAIR_, false>), grid, dim3(64 * NW_), 0, \
+                       x, pe, qw[0], sc[0], qz[0], qw[1], sc[1], qz[1], zoff, y, M, K, N, ntiles);                \
+    } while (0)
 #define ST_I4MM(KCU_, GW_, NW_) ST_I4MM_P(KCU_, GW_, NW_, false)
     // gate/up with both sources in a wave: wpt is then waves per tile pair
     if constexpr (NSRC == 2 && GS != 64) {  // (group 64 with two sources per wave spills)
