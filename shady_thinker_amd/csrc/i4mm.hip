@@ -241,7 +241,10 @@ __global__ __launch_bounds__(64 * NW) void i4mm_kernel(const void *__restrict__ 
     // Rows already in B order: the chunk is copied. With f32 x, threads
     // tid < KCU 16 also copy the chunk's 2^e factors (unit tid / 16, token tid % 16).
     const int nrows = F32X ? 2 * M : M;
-    constexpr int XS = NW <= 12 ? 2 : 1;
+    // x is loaded XS chunks ahead (register set c % XS holds chunk c): two
+    // where the registers allow it (12-wave workgroups, or 2-unit chunks),
+    // else one, which leaves each chunk's staging waiting for its x
+    constexpr int XS = (NW <= 12 || KCU <= 2) ? 2 : 1;
     u32x4 xr2[XS][RAW ? 2 * XLR : XL];
     unsigned pr2[XS];
     auto load_x = [&](u32x4 (&xr)[RAW ? 2 * XLR : XL], unsigned &pr, int c) {
@@ -444,7 +447,7 @@ __global__ __launch_bounds__(64 * NW) void i4mm_kernel(const void *__restrict__ 
         }
     };
 
-    // Chunk c: its x was loaded during chunk c - 1 and staged into LDS buffer
+    // Chunk c: its x was loaded during chunk c - XS and staged into LDS buffer
     // c % 2 at the end of chunk c - 1; its weights were loaded during chunk
     // c - 2 into ring slot c % 3. Six chunks per trip so that every buffer
     // index is compile-time; loads are unconditional (past the end they read
