@@ -82,8 +82,13 @@ __global__ __launch_bounds__(kThreads) void i8mm_kernel(const _Float16 *__restri
 
     // x chunk c: thread item i = j * kThreads + tid is row i / (kKC / 8),
     // 8 halves at column 8 (i % (kKC / 8)). Rows >= M and k >= K read 0.
-    u32x4 xr[XL];
-    auto load_x = [&](int c) {
+    // x is loaded XS chunks ahead (register set c % XS holds chunk c): two
+    // where the registers allow it, so that a chunk's staging does not wait
+    // for a load issued in the same chunk (32 tokens with 4 groups per wave:
+    // one, two spilled)
+    constexpr int XS = (MB == 2 && GW == 4) ? 1 : 2;
+    u32x4 xr2[XS][XL];
+    auto load_x = [&](u32x4 (&xr)[XL], int c) {
 #pragma unroll
         for (int j = 0; j < XL; ++j) {
             const int i = j * kThreads + tid;
@@ -92,7 +97,7 @@ __global__ __launch_bounds__(kThreads) void i8mm_kernel(const _Float16 *__restri
             xr[j] = __builtin_amdgcn_raw_buffer_load_b128(rx, off, 0, 0);
         }
     };
-    auto store_x = [&](_Float16 *xs) {
+    auto store_x = [&](const u32x4 (&xr)[XL], _Float16 *xs) {
 #pragma unroll
         for (int j = 0; j < XL; ++j) {
             const int i = j * kThreads + tid;
@@ -134,24 +139,25 @@ __global__ __launch_bounds__(kThreads) void i8mm_kernel(const _Float16 *__restri
                 }
     };
 
-    load_x(0);
+    load_x(xr2[0], 0);
+    if constexpr (XS == 2) load_x(xr2[XS - 1], 1);
     load_w(wr[0], 0);
-    store_x(xs0);
+    store_x(xr2[0], xs0);
     lds_barrier();
     // Two chunks per trip so that buffer indices are compile-time. The loads
     // of the next chunk are unconditional (past the last chunk they read
     // nothing), so the compiler's wait counts are the same on every path.
     for (int c = 0; c < nch; c += 2) {
-        load_x(c + 1);
+        load_x(xr2[0], c + XS);  // (set 0 was stored for chunk c at the end of chunk c - 1)
         load_w(wr[1], c + 1);
         if (active) compute(xs0, wr[0]);  // a wave without a tile skips the work (and its LDS reads)
-        store_x(xs1);
+        store_x(xr2[XS - 1], xs1);  // chunk c + 1
         lds_barrier();
         if (c + 1 >= nch) break;
-        load_x(c + 2);
+        load_x(xr2[XS - 1], c + 1 + XS);
         load_w(wr[0], c + 2);
         if (active) compute(xs1, wr[1]);
-        store_x(xs0);
+        store_x(xr2[0], xs0);  // chunk c + 2
         lds_barrier();
     }
 
