@@ -8,8 +8,9 @@
 //  * Exact products: (q - z) is an integer in [-15, 15], exact in f16 (the
 //    f16 1024 bias: 1024 + q, minus 1024 + z). f16 x is used as is. f32 x is
 //    split per token and per 128 k: x 2^-e (2^e just above the block's
-//    largest |x|) = hi + lo, two f16 rows of the MFMA A operand (about 22
-//    significant bits), as each chunk of x is staged into LDS (with
+//    largest |x|) = hi + lo, two f16 rows of the MFMA A operand (about 21
+//    significant bits: hi its top 11 bits, lo the rest rounded toward
+//    zero), as each chunk of x is staged into LDS (with
 //    act-order, by a pre-pass into the context workspace). Every
 //    product is exact in f32; each 64 (or 128) k block sums into a fresh
 //    accumulator that is then scaled by s 2^e in f32.
@@ -78,17 +79,43 @@ __device__ __forceinline__ u32x4 to_b_order(u32x4 a) {
     return r;
 }
 
-template <int CTRL>
-__device__ __forceinline__ float dpp_f(float v) {
-    return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), CTRL, 0xF, 0xF, true));
+// 8 f32 x (k0..k7) times 2^-e (|x 2^-e| < 1) -> hi and lo f16 in the
+// order of word_to_b, |x 2^-e - hi - lo| < 2^-20 |x 2^-e| + 2^-24:
+// hi keeps the top 11 significant bits of x 2^-e (a mask, so hi - x 2^-e is
+// exact in f32 and hi is exact in f16), lo is the rest rounded toward zero
+// to f16. v_cvt_pkrtz packs two of them per instruction, paired as the B
+// fragment wants them (k0 k4, k1 k5, k2 k6, k3 k7).
+__device__ __forceinline__ void split_hi_lo(const float (&v)[8], float down, u32x4 &H, u32x4 &L) {
+    float hi[8], lo[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+        const float xs = v[e] * down;
+        hi[e] = __uint_as_float(__float_as_uint(xs) & 0xFFFFE000u);
+        lo[e] = xs - hi[e];
+    }
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+        H[e] = __builtin_bit_cast(unsigned, __builtin_amdgcn_cvt_pkrtz(hi[e], hi[e + 4]));
+        L[e] = __builtin_bit_cast(unsigned, __builtin_amdgcn_cvt_pkrtz(lo[e], lo[e + 4]));
+    }
 }
-// max over the 16 lanes of a DPP row
-__device__ __forceinline__ float row_max(float v) {
-    v = fmaxf(v, dpp_f<0xB1>(v));   // quad_perm [1,0,3,2]
-    v = fmaxf(v, dpp_f<0x4E>(v));   // quad_perm [2,3,0,1]
-    v = fmaxf(v, dpp_f<0x141>(v));  // row_half_mirror
-    v = fmaxf(v, dpp_f<0x140>(v));  // row_mirror
-    return v;
+
+template <int CTRL>
+__device__ __forceinline__ unsigned dpp_u(unsigned v) {
+    return (unsigned)__builtin_amdgcn_mov_dpp((int)v, CTRL, 0xF, 0xF, true);
+}
+// 2^e just above the largest |x| of a 128-k unit (its 16 lanes hold 8 k
+// each): e = 0 for an all-zero unit. The maximum is taken on the bit
+// patterns of |x| (ordered like the values), so no canonicalizing float max.
+__device__ __forceinline__ int unit_exponent(const float (&v)[8]) {
+    unsigned m = 0;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) m = max(m, __float_as_uint(v[e]) & 0x7FFFFFFFu);
+    m = max(m, dpp_u<0xB1>(m));   // quad_perm [1,0,3,2]
+    m = max(m, dpp_u<0x4E>(m));   // quad_perm [2,3,0,1]
+    m = max(m, dpp_u<0x141>(m));  // row_half_mirror
+    m = max(m, dpp_u<0x140>(m));  // row_mirror
+    return m ? __builtin_amdgcn_frexp_expf(__uint_as_float(m)) : 0;  // |x| < 2^e
 }
 
 // silu(v) = v / (1 + exp(-v)) (fused_gate_up_silu_4t.wgsl)
@@ -126,28 +153,12 @@ __global__ __launch_bounds__(256) void i4mm_prep_kernel(const float *__restrict_
         b = *reinterpret_cast<const f32x4 *>(x + (size_t)t * K + k + 4);
     }
     const float v[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
-    float amax = 0.f;
-#pragma unroll
-    for (int e = 0; e < 8; ++e) amax = fmaxf(amax, fabsf(v[e]));
-    amax = row_max(amax);
-    const int ex = amax > 0.f ? __builtin_amdgcn_frexp_expf(amax) : 0;  // amax < 2^ex
-    const float down = __builtin_amdgcn_ldexpf(1.0f, -ex);
-    _Float16 hi[8], lo[8];
-#pragma unroll
-    for (int e = 0; e < 8; ++e) {
-        const float xv = v[e] * down;
-        hi[e] = (_Float16)xv;
-        lo[e] = (_Float16)(xv - (float)hi[e]);
-    }
+    const int ex = unit_exponent(v);
     u32x4 H, L;
-#pragma unroll
-    for (int e = 0; e < 4; ++e) {
-        H[e] = (unsigned)__builtin_bit_cast(uint16_t, hi[2 * e]) | ((unsigned)__builtin_bit_cast(uint16_t, hi[2 * e + 1]) << 16);
-        L[e] = (unsigned)__builtin_bit_cast(uint16_t, lo[2 * e]) | ((unsigned)__builtin_bit_cast(uint16_t, lo[2 * e + 1]) << 16);
-    }
+    split_hi_lo(v, __builtin_amdgcn_ldexpf(1.0f, -ex), H, L);
     if (!ok) return;
-    *reinterpret_cast<u32x4 *>(xp + (size_t)(2 * t) * K + k) = to_b_order(H);
-    *reinterpret_cast<u32x4 *>(xp + (size_t)(2 * t + 1) * K + k) = to_b_order(L);
+    *reinterpret_cast<u32x4 *>(xp + (size_t)(2 * t) * K + k) = H;
+    *reinterpret_cast<u32x4 *>(xp + (size_t)(2 * t + 1) * K + k) = L;
     if (l == 0) pe[(size_t)t * units + u] = __builtin_amdgcn_ldexpf(1.0f, ex);
 }
 
@@ -280,6 +291,10 @@ __global__ __launch_bounds__(64 * NW) void i4mm_kernel(const void *__restrict__ 
 #pragma unroll
             for (int j = 0; j < XLR; ++j) {
                 const int i = j * kThr + tid;
+                // A wave whose items all belong to tokens >= M (or lie past
+                // the chunk's items) skips them: only output rows that are
+                // never written read those rows of xs (a uniform branch)
+                if ((j * kThr + wave * 64) / (kKC / 8) >= M) continue;
                 // (each word through a scalar first: hipcc's __builtin_bit_cast
                 // of an ext_vector component reads component 0)
                 const u32x4 a = xr[2 * j], b = xr[2 * j + 1];
@@ -287,26 +302,14 @@ __global__ __launch_bounds__(64 * NW) void i4mm_kernel(const void *__restrict__ 
                 float v[8];
 #pragma unroll
                 for (int e = 0; e < 8; ++e) v[e] = __uint_as_float(wv[e]);
-                float amax = 0.f;
-#pragma unroll
-                for (int e = 0; e < 8; ++e) amax = fmaxf(amax, fabsf(v[e]));
-                amax = row_max(amax);  // every lane takes part (items past the end read zeros)
-                const int ex = amax > 0.f ? __builtin_amdgcn_frexp_expf(amax) : 0;
-                const float down = __builtin_amdgcn_ldexpf(1.0f, -ex);
-                unsigned hw[4], lw[4];
-#pragma unroll
-                for (int e = 0; e < 4; ++e) {
-                    const float x0 = v[2 * e] * down, x1 = v[2 * e + 1] * down;
-                    const _Float16 h0 = (_Float16)x0, h1 = (_Float16)x1;
-                    const _Float16 l0 = (_Float16)(x0 - (float)h0), l1 = (_Float16)(x1 - (float)h1);
-                    hw[e] = (unsigned)__builtin_bit_cast(uint16_t, h0) | ((unsigned)__builtin_bit_cast(uint16_t, h1) << 16);
-                    lw[e] = (unsigned)__builtin_bit_cast(uint16_t, l0) | ((unsigned)__builtin_bit_cast(uint16_t, l1) << 16);
-                }
-                const u32x4 H = {hw[0], hw[1], hw[2], hw[3]}, L = {lw[0], lw[1], lw[2], lw[3]};
+                // (every lane of the wave takes part: items past the end read zeros)
+                const int ex = unit_exponent(v);
+                u32x4 H, L;
+                split_hi_lo(v, __builtin_amdgcn_ldexpf(1.0f, -ex), H, L);
                 if (RITEMS % kThr == 0 || i < RITEMS) {
                     const int t = i / (kKC / 8), kq = i % (kKC / 8);
-                    *reinterpret_cast<u32x4 *>(&xs[(2 * t) * kPitch + 8 * kq]) = to_b_order(H);
-                    *reinterpret_cast<u32x4 *>(&xs[(2 * t + 1) * kPitch + 8 * kq]) = to_b_order(L);
+                    *reinterpret_cast<u32x4 *>(&xs[(2 * t) * kPitch + 8 * kq]) = H;
+                    *reinterpret_cast<u32x4 *>(&xs[(2 * t + 1) * kPitch + 8 * kq]) = L;
                     if ((kq & 15) == 0) ps[(kq >> 4) * 16 + t] = __builtin_amdgcn_ldexpf(1.0f, ex);
                 }
             }
