@@ -117,6 +117,7 @@ typedef enum {
     ST_TUNE_I4MM_WAVES,        /* f16-MFMA GPTQ decode: 16 forces 16-wave workgroups (default: 12 when the tiles use at most 12) */
     ST_TUNE_I4MM_PAIR,         /* f16-MFMA gate/up: 0 gives each wave one source (default 1: both sources of a tile per wave) */
     ST_TUNE_I4MM_PREPASS,      /* f16-MFMA GPTQ decode, f32 x: 1 splits x in a pre-pass launch (default: in the kernel, unless act-order) */
+    ST_TUNE_I4MM_SPLIT_TILES,  /* f16-MFMA GPTQ decode on at most one 16-column tile per CU: tiles per workgroup, K split across workgroups (0: limb kernels) */
     ST_TUNE_COUNT
 } st_tune;
 int st_context_set_tune(st_context *ctx, int knob, int value);

@@ -23,7 +23,8 @@ ST_FLAG_TILED = 0x2
 # st_tune (include/shady_hip.h): kernel-path overrides of one context
 TUNE_KNOBS = ("DECODE_KERNEL", "STAGE_MODE", "STAGE_ROUNDS", "WAVES", "NO_COOP", "ONE_TILE", "NO_CHUNK", "NO_KSPLIT",
               "SPLIT_TILES_CU", "TOKEN_BLOCK", "I4MM_MIN_M", "I4MM_MIN_TILES", "I8MM_MIN_M", "GEMM_CB", "GEMM_NO_SPLIT",
-              "STREAM_WAVES", "STREAM_TILES_WG", "STREAM_SYNC", "SPLIT_REDUCE_KERNEL", "I4MM_WAVES", "I4MM_PAIR", "I4MM_PREPASS")
+              "STREAM_WAVES", "STREAM_TILES_WG", "STREAM_SYNC", "SPLIT_REDUCE_KERNEL", "I4MM_WAVES", "I4MM_PAIR", "I4MM_PREPASS",
+              "I4MM_SPLIT_TILES")
 TUNE = {name: i for i, name in enumerate(TUNE_KNOBS)}
 
 STATUS_NAMES = {

@@ -107,6 +107,10 @@ inline void launch(st_context *ctx, F kernel, dim3 grid, dim3 block, size_t lds,
 int int8_mm_f16(st_context *ctx, const void *x, const int8_t *w, const float *scale, float *y, int M, int K, int N);
 // Multi-token GPTQ int4 matvec / gate-up on f16 MFMA (i4mm.hip), tiled
 // weights (act-order through perm, or NULL), M <= 16; checked by the caller.
+// -1: not taken (a K split whose partials do not fit the workspace).
+// On at most one 16-column tile per CU it takes groups of kI4mmSplitTiles
+// tiles with K split across workgroups (0: the integer-limb kernels).
+constexpr int kI4mmSplitTiles = 8;
 int int4_mm_f16(st_context *ctx, const void *x, bool x_f32, const int32_t *perm, const uint32_t *const qw[2],
                 const uint16_t *const sc[2], const uint32_t *const qz[2], int zoff, float *y, int M, int K, int N,
                 int gs, int nsrc);

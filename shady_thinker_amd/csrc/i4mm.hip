@@ -45,6 +45,7 @@ constexpr int kTileN = 16;
 constexpr int kRsrcWord3 = 0x00020000;     // raw 32-bit buffer data (gfx9-class)
 constexpr unsigned kNoLoad = 0x80000000u;  // buffer offset past every resource: reads 0, touches no memory
 constexpr int kMaxTilesPerWg = 8;
+constexpr int kMaxSplit = 16;  // K slices of a split launch
 
 // v_and_or_b32 with both constants in registers (a VOP3 takes no literal).
 __device__ __forceinline__ unsigned and_or(unsigned a, unsigned m, unsigned c) {
@@ -179,7 +180,7 @@ __global__ __launch_bounds__(64 * NW) void i4mm_kernel(const void *__restrict__ 
                                                         const uint16_t *__restrict__ sc0, const uint32_t *__restrict__ qz0,
                                                         const uint32_t *__restrict__ qw1, const uint16_t *__restrict__ sc1,
                                                         const uint32_t *__restrict__ qz1, int zoff, float *__restrict__ y,
-                                                        int M, int K, int N, int ntiles) {
+                                                        int M, int K, int N, int ntiles, float *__restrict__ part, int ks) {
     // XM: 0 f16 x; 1 f32 x split by i4mm_prep_kernel (hi / lo rows and
     // factors in the workspace); 2 f32 x split here, at staging, with the
     // same arithmetic (no pre-pass launch)
@@ -218,14 +219,19 @@ __global__ __launch_bounds__(64 * NW) void i4mm_kernel(const void *__restrict__ 
     // weight, scale and zero resources in VGPRs, every load of them in a
     // waterfall loop.
     const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const int t0 = (int)((long long)blockIdx.x * ntiles / gridDim.x);
-    const int t1 = (int)((long long)(blockIdx.x + 1) * ntiles / gridDim.x);
+    // K split (ks > 1): workgroup b takes K slice b % ks of tile group b / ks
+    const int kslice = blockIdx.x % ks, ngrp = gridDim.x / ks, grp = blockIdx.x / ks;
+    const int t0 = (int)((long long)grp * ntiles / ngrp);
+    const int t1 = (int)((long long)(grp + 1) * ntiles / ngrp);
     const int tb = PAIR ? wave / S : wave / (NSRC * S), src = PAIR ? 0 : (wave / S) % NSRC, slice = wave % S;
     const bool active = t0 + tb < t1;
     const int T = min(t0 + tb, ntiles - 1);
     const int G = K / GS;
     const int units = K / 128;
-    const int nch = (units + KCU - 1) / KCU;
+    // this slice's chunks [cb, ce), its units below uend, its k below kend
+    const int nch_all = (units + KCU - 1) / KCU;
+    const int cb = kslice * nch_all / ks, ce = (kslice + 1) * nch_all / ks;
+    const int uend = min(units, ce * KCU), kend = min(K, ce * kKC);
     const int q = lane >> 4, r16 = lane & 15;
     const int n = min(kTileN * T + r16, N - 1);  // this lane's column (the last tile's padding repeats N - 1)
 
@@ -264,7 +270,7 @@ __global__ __launch_bounds__(64 * NW) void i4mm_kernel(const void *__restrict__ 
             for (int j = 0; j < XLR; ++j) {
                 const int i = j * kThr + tid;
                 const int t = i / (kKC / 8), k = c * kKC + 8 * (i % (kKC / 8));
-                const bool ok = i < RITEMS && t < M && k < K;
+                const bool ok = i < RITEMS && t < M && k < kend;
                 const unsigned o = ok ? (unsigned)(t * K + k) * 4u : kNoLoad;
                 xr[2 * j] = __builtin_amdgcn_raw_buffer_load_b128(rx, o, 0, 0);
                 xr[2 * j + 1] = __builtin_amdgcn_raw_buffer_load_b128(rx, ok ? o + 16u : kNoLoad, 0, 0);
@@ -275,12 +281,12 @@ __global__ __launch_bounds__(64 * NW) void i4mm_kernel(const void *__restrict__ 
         for (int j = 0; j < XL; ++j) {
             const int i = j * kThr + tid;
             const int row = i / (kKC / 8), k = c * kKC + 8 * (i % (kKC / 8));
-            const bool ok = i < XITEMS && row < nrows && k < K;
+            const bool ok = i < XITEMS && row < nrows && k < kend;
             xr[j] = __builtin_amdgcn_raw_buffer_load_b128(rx, ok ? (unsigned)(row * K + k) * 2u : kNoLoad, 0, 0);
         }
         if constexpr (F32X) {
             const int t = tid & 15, u = c * KCU + (tid >> 4);
-            const bool ok = tid < KCU * 16 && t < M && u < units;
+            const bool ok = tid < KCU * 16 && t < M && u < uend;
             pr = __builtin_amdgcn_raw_buffer_load_b32(rp, ok ? (unsigned)(t * units + u) * 4u : kNoLoad, 0, 0);
         }
     };
@@ -338,7 +344,7 @@ __global__ __launch_bounds__(64 * NW) void i4mm_kernel(const void *__restrict__ 
         for (int gi = 0; gi < GW; ++gi) {
             Unit<GS> &du = dsts[gi][ps];
             const int u = c * KCU + slice * GW + gi;
-            const bool ok = active && u < units;
+            const bool ok = active && u < uend;
             if constexpr (GS == 64) {
                 unsigned o0 = ok ? (unsigned)(((T * G + 2 * u) * 64 + lane) * 8) : kNoLoad;
                 asm volatile("" : "+v"(o0));
@@ -455,10 +461,10 @@ __global__ __launch_bounds__(64 * NW) void i4mm_kernel(const void *__restrict__ 
     // c - 2 into ring slot c % 3. Six chunks per trip so that every buffer
     // index is compile-time; loads are unconditional (past the end they read
     // nothing), so the compiler's wait counts are the same on every path.
-    load_x(xr2[0], pr2[0], 0);
-    if constexpr (XS == 2) load_x(xr2[1], pr2[1], 1);
-    load_u(ur[0], 0);
-    load_u(ur[1], 1);
+    load_x(xr2[0], pr2[0], cb);
+    if constexpr (XS == 2) load_x(xr2[1], pr2[1], cb + 1);
+    load_u(ur[0], cb);
+    load_u(ur[1], cb + 1);
     store_x(xr2[0], pr2[0], xs0, ps0);
     lds_barrier();
     auto chunk = [&](auto P, int c) {
@@ -472,17 +478,17 @@ __global__ __launch_bounds__(64 * NW) void i4mm_kernel(const void *__restrict__ 
         store_x(xr2[(p + 1) % XS], pr2[(p + 1) % XS], p % 2 ? xs0 : xs1, p % 2 ? ps0 : ps1);  // chunk c + 1
         lds_barrier();
     };
-    for (int c = 0; c < nch; c += 6) {
+    for (int c = cb; c < ce; c += 6) {
         chunk(std::integral_constant<int, 0>{}, c);
-        if (c + 1 >= nch) break;
+        if (c + 1 >= ce) break;
         chunk(std::integral_constant<int, 1>{}, c + 1);
-        if (c + 2 >= nch) break;
+        if (c + 2 >= ce) break;
         chunk(std::integral_constant<int, 2>{}, c + 2);
-        if (c + 3 >= nch) break;
+        if (c + 3 >= ce) break;
         chunk(std::integral_constant<int, 3>{}, c + 3);
-        if (c + 4 >= nch) break;
+        if (c + 4 >= ce) break;
         chunk(std::integral_constant<int, 4>{}, c + 4);
-        if (c + 5 >= nch) break;
+        if (c + 5 >= ce) break;
         chunk(std::integral_constant<int, 5>{}, c + 5);
     }
 
@@ -514,24 +520,53 @@ __global__ __launch_bounds__(64 * NW) void i4mm_kernel(const void *__restrict__ 
                     v[sr] += red[((((tb * NSRC + sr) * S + sl) * MB + mb) * YV + i) * 64 + lane];
             }
             const int m = F32X ? TPB * mb + 2 * q + i : 16 * mb + 4 * q + i;
-            if (m < M) y[(size_t)m * N + nc] = NSRC == 2 ? silu_f(v[0]) * v[1] : v[0];
+            if (m >= M) continue;
+            if (ks > 1) {  // the slice's sums, to i4mm_reduce_kernel
+#pragma unroll
+                for (int sr = 0; sr < NSRC; ++sr) part[((size_t)(kslice * NSRC + sr) * M + m) * N + nc] = v[sr];
+            } else {
+                y[(size_t)m * N + nc] = NSRC == 2 ? silu_f(v[0]) * v[1] : v[0];
+            }
         }
+}
+
+// K split: y = epilogue(sum over slices s < ks of part[s][src]), the slices
+// added in order (deterministic), the epilogue silu(gate) * up for two sources.
+template <int NSRC>
+__global__ __launch_bounds__(256) void i4mm_reduce_kernel(const float *__restrict__ part, float *__restrict__ y, int MN,
+                                                          int ks) {
+    const int idx = blockIdx.x * 256 + threadIdx.x;
+    if (idx >= MN) return;
+    float t[kMaxSplit][NSRC];  // every slice's load issued before the first add
+#pragma unroll
+    for (int s = 0; s < kMaxSplit; ++s)
+#pragma unroll
+        for (int sr = 0; sr < NSRC; ++sr) t[s][sr] = s < ks ? part[(size_t)(s * NSRC + sr) * MN + idx] : 0.f;
+    float v[NSRC];
+#pragma unroll
+    for (int sr = 0; sr < NSRC; ++sr) {
+        v[sr] = 0.f;
+#pragma unroll
+        for (int s = 0; s < kMaxSplit; ++s)
+            if (s < ks) v[sr] += t[s][sr];
+    }
+    y[idx] = NSRC == 2 ? silu_f(v[0]) * v[1] : v[0];
 }
 
 template <int XM, int NSRC, int MB, int GS>
 int launch_gs(st_context *ctx, const void *x, const float *pe, const uint32_t *const *qw, const uint16_t *const *sc,
               const uint32_t *const *qz, int zoff, float *y, int M, int K, int N, int ntiles, int G, int wpt, int nw,
-              bool pair) {
-    const dim3 grid(G);
+              bool pair, float *part, int ks) {
+    const dim3 grid(G * ks);
     const bool hz = qz[0] || (NSRC == 2 && qz[1]);
 #define ST_I4MM_P(KCU_, GW_, NW_, PAIR_)                                                                           \
     do {                                                                                                           \
         if (hz)                                                                                                    \
             st::launch(ctx, (i4mm_kernel<XM, NSRC, MB, GS, KCU_, GW_, NW_, PAIR_, true>), grid, dim3(64 * NW_), 0,  \
-                       x, pe, qw[0], sc[0], qz[0], qw[1], sc[1], qz[1], zoff, y, M, K, N, ntiles);                \
+                       x, pe, qw[0], sc[0], qz[0], qw[1], sc[1], qz[1], zoff, y, M, K, N, ntiles, part, ks);    \
         else                                                                                                       \
             st::launch(ctx, (i4mm_kernel<XM, NSRC, MB, GS, KCU_, GW_, NW_, PAIR_, false>), grid, dim3(64 * NW_), 0, \
-                       x, pe, qw[0], sc[0], qz[0], qw[1], sc[1], qz[1], zoff, y, M, K, N, ntiles);                \
+                       x, pe, qw[0], sc[0], qz[0], qw[1], sc[1], qz[1], zoff, y, M, K, N, ntiles, part, ks);    \
     } while (0)
 #define ST_I4MM(KCU_, GW_, NW_) ST_I4MM_P(KCU_, GW_, NW_, false)
     // gate/up with both sources in a wave: wpt is then waves per tile pair
@@ -587,24 +622,29 @@ __global__ __launch_bounds__(256) void i4mm_gather_kernel(const uint16_t *__rest
 template <int XM, int NSRC, int MB>
 int launch_mb(st_context *ctx, const void *x, const float *pe, const uint32_t *const *qw, const uint16_t *const *sc,
               const uint32_t *const *qz, int zoff, float *y, int M, int K, int N, int gs, int ntiles, int G, int wpt,
-              int nw, bool pair) {
+              int nw, bool pair, float *part, int ks) {
     switch (gs) {
-        case 64: return launch_gs<XM, NSRC, MB, 64>(ctx, x, pe, qw, sc, qz, zoff, y, M, K, N, ntiles, G, wpt, nw, pair);
+        case 64:
+            return launch_gs<XM, NSRC, MB, 64>(ctx, x, pe, qw, sc, qz, zoff, y, M, K, N, ntiles, G, wpt, nw, pair, part, ks);
         case 128:
-            return launch_gs<XM, NSRC, MB, 128>(ctx, x, pe, qw, sc, qz, zoff, y, M, K, N, ntiles, G, wpt, nw, pair);
+            return launch_gs<XM, NSRC, MB, 128>(ctx, x, pe, qw, sc, qz, zoff, y, M, K, N, ntiles, G, wpt, nw, pair, part, ks);
         default:
-            return launch_gs<XM, NSRC, MB, 256>(ctx, x, pe, qw, sc, qz, zoff, y, M, K, N, ntiles, G, wpt, nw, pair);
+            return launch_gs<XM, NSRC, MB, 256>(ctx, x, pe, qw, sc, qz, zoff, y, M, K, N, ntiles, G, wpt, nw, pair, part, ks);
     }
 }
 
 template <int XM, int NSRC>
 int launch_src(st_context *ctx, const void *x, const float *pe, const uint32_t *const *qw, const uint16_t *const *sc,
                const uint32_t *const *qz, int zoff, float *y, int M, int K, int N, int gs, int ntiles, int G, int wpt,
-               int nw, bool pair) {
+               int nw, bool pair, float *part, int ks) {
     // tokens per 16-row block: 8 (f32 x: hi and lo rows) or 16
     const int mb = (M * (XM ? 2 : 1) + 15) / 16;
-    return mb <= 1 ? launch_mb<XM, NSRC, 1>(ctx, x, pe, qw, sc, qz, zoff, y, M, K, N, gs, ntiles, G, wpt, nw, pair)
-                   : launch_mb<XM, NSRC, 2>(ctx, x, pe, qw, sc, qz, zoff, y, M, K, N, gs, ntiles, G, wpt, nw, pair);
+    int rc = mb <= 1 ? launch_mb<XM, NSRC, 1>(ctx, x, pe, qw, sc, qz, zoff, y, M, K, N, gs, ntiles, G, wpt, nw, pair, part, ks)
+                     : launch_mb<XM, NSRC, 2>(ctx, x, pe, qw, sc, qz, zoff, y, M, K, N, gs, ntiles, G, wpt, nw, pair, part, ks);
+    if (rc || ks == 1) return rc;
+    const int mn = M * N;
+    st::launch(ctx, (i4mm_reduce_kernel<NSRC>), dim3((mn + 255) / 256), dim3(256), 0, part, y, mn, ks);
+    return st::launch_check("i4mm_reduce_kernel");
 }
 
 }  // namespace
@@ -613,6 +653,9 @@ namespace st {
 
 // Arguments are checked by the entry points (tiled weights, M <= 16, K %
 // 128 == 0, K % group_size == 0, N % 8 == 0, alignment, 32-bit offsets).
+// Returns -1, having launched nothing, when the shape would split K and the
+// slices' partial sums do not fit the workspace (the caller then takes the
+// integer-limb kernels).
 // perm (act-order, may be NULL): x is read as x[:, perm[k]], by the f32
 // pre-pass or, for f16 x, by a gather pass into the workspace.
 int int4_mm_f16(st_context *ctx, const void *x, bool x_f32, const int32_t *perm, const uint32_t *const qw[2],
@@ -620,7 +663,12 @@ int int4_mm_f16(st_context *ctx, const void *x, bool x_f32, const int32_t *perm,
                 int gs, int nsrc) {
     const int ntiles = (N + kTileN - 1) / kTileN;
     const int maxt = kMaxTilesPerWg / nsrc;  // tiles per workgroup: each tile (and source) keeps >= 2 waves
-    const int G = std::max(std::min(ctx->num_cus, ntiles), (ntiles + maxt - 1) / maxt);
+    // At most one tile per CU: groups of split_tiles tiles, K split across
+    // workgroups so that the grid fills the CUs (0: one workgroup per tile)
+    const int split_tiles =
+        ntiles <= ctx->num_cus ? std::min(tune(ctx, ST_TUNE_I4MM_SPLIT_TILES, kI4mmSplitTiles), maxt) : 0;
+    int G = std::max(std::min(ctx->num_cus, ntiles), (ntiles + maxt - 1) / maxt);
+    if (split_tiles > 0) G = (ntiles + split_tiles - 1) / split_tiles;
     const int tbmax = (ntiles + G - 1) / G;
     int wpt = 2;  // waves per tile and source: a power of two, wpt * nsrc * tbmax <= 16
     while (wpt < 8 && 2 * wpt * nsrc * tbmax <= kWaves) wpt *= 2;
@@ -646,6 +694,22 @@ int int4_mm_f16(st_context *ctx, const void *x, bool x_f32, const int32_t *perm,
     // f32 x without act-order: split inside the kernel (XM 2); with
     // act-order, or when the setting asks for it, by the pre-pass (XM 1)
     const bool split_in = x_f32 && !perm && tune(ctx, ST_TUNE_I4MM_PREPASS, 0) != 1;
+    // K slices (whole chunks each) and their f32 partials in the workspace,
+    // after what the pre-pass or the gather writes there
+    int ks = 1;
+    float *part = nullptr;
+    if (split_tiles > 0) {
+        const int kcu = pair ? (wpt >= 4 ? 4 : 2) : (wpt >= 8 && gs != 64 ? 8 : (wpt >= 4 ? 4 : 2));
+        const int nch = (K / 128 + kcu - 1) / kcu;
+        ks = std::max(1, std::min({ctx->num_cus / G, kMaxSplit, nch}));
+        if (ks > 1) {
+            const size_t pre = x_f32 && !split_in ? (((size_t)2 * M * K * 2 + 255) & ~size_t(255)) + (size_t)M * (K / 128) * 4
+                                                  : (perm ? (size_t)M * K * 2 : 0);
+            const size_t off = (pre + 255) & ~size_t(255);
+            if (!ctx->ws || off + (size_t)ks * nsrc * M * N * sizeof(float) > ctx->ws_bytes) return -1;  // not taken
+            part = reinterpret_cast<float *>(reinterpret_cast<char *>(ctx->ws) + off);
+        }
+    }
     if (x_f32 && !split_in) {  // the pre-pass writes [2M, K] f16 rows and [M, K / 128] factors into the workspace
         const size_t xbytes = ((size_t)2 * M * K * 2 + 255) & ~size_t(255);
         if (!ctx->ws || xbytes + (size_t)M * (K / 128) * 4 > ctx->ws_bytes)
@@ -666,13 +730,13 @@ int int4_mm_f16(st_context *ctx, const void *x, bool x_f32, const int32_t *perm,
         xa = xg;
     }
     if (split_in)
-        return nsrc == 2 ? launch_src<2, 2>(ctx, xa, pe, qw, sc, qz, zoff, y, M, K, N, gs, ntiles, G, wpt, nw, pair)
-                         : launch_src<2, 1>(ctx, xa, pe, qw, sc, qz, zoff, y, M, K, N, gs, ntiles, G, wpt, nw, pair);
+        return nsrc == 2 ? launch_src<2, 2>(ctx, xa, pe, qw, sc, qz, zoff, y, M, K, N, gs, ntiles, G, wpt, nw, pair, part, ks)
+                         : launch_src<2, 1>(ctx, xa, pe, qw, sc, qz, zoff, y, M, K, N, gs, ntiles, G, wpt, nw, pair, part, ks);
     if (nsrc == 2)
-        return x_f32 ? launch_src<1, 2>(ctx, xa, pe, qw, sc, qz, zoff, y, M, K, N, gs, ntiles, G, wpt, nw, pair)
-                     : launch_src<0, 2>(ctx, xa, pe, qw, sc, qz, zoff, y, M, K, N, gs, ntiles, G, wpt, nw, pair);
-    return x_f32 ? launch_src<1, 1>(ctx, xa, pe, qw, sc, qz, zoff, y, M, K, N, gs, ntiles, G, wpt, nw, pair)
-                 : launch_src<0, 1>(ctx, xa, pe, qw, sc, qz, zoff, y, M, K, N, gs, ntiles, G, wpt, nw, pair);
+        return x_f32 ? launch_src<1, 2>(ctx, xa, pe, qw, sc, qz, zoff, y, M, K, N, gs, ntiles, G, wpt, nw, pair, part, ks)
+                     : launch_src<0, 2>(ctx, xa, pe, qw, sc, qz, zoff, y, M, K, N, gs, ntiles, G, wpt, nw, pair, part, ks);
+    return x_f32 ? launch_src<1, 1>(ctx, xa, pe, qw, sc, qz, zoff, y, M, K, N, gs, ntiles, G, wpt, nw, pair, part, ks)
+                 : launch_src<0, 1>(ctx, xa, pe, qw, sc, qz, zoff, y, M, K, N, gs, ntiles, G, wpt, nw, pair, part, ks);
 }
 
 }  // namespace st

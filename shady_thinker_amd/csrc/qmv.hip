@@ -79,14 +79,17 @@ bool use_i4mm(const st_context *ctx, const QmvParams &p, bool tiled, int xm) {
     const int ntiles = (p.N + kTileN - 1) / kTileN;
     const int min_m = std::max(2, st::tune(ctx, ST_TUNE_I4MM_MIN_M, kI4mmMinM));
     const int min_tiles = st::tune(ctx, ST_TUNE_I4MM_MIN_TILES, ctx->num_cus + 1);
-    return tiled && (xm == XM_F32 || xm == XM_F16) && p.M <= 16 && p.M >= min_m && ntiles >= min_tiles &&
+    const bool few = ntiles <= ctx->num_cus && st::tune(ctx, ST_TUNE_I4MM_SPLIT_TILES, st::kI4mmSplitTiles) > 0;
+    return tiled && (xm == XM_F32 || xm == XM_F16) && p.M <= 16 && p.M >= min_m && (ntiles >= min_tiles || few) &&
            p.K % 128 == 0 && (size_t)ntiles * kTileN * p.K / 2 < (size_t(1) << 31);
 }
 
 int launch_i4(st_context *ctx, QmvParams &p, bool tiled, int nsrc, int xm) {
-    if (use_i4mm(ctx, p, tiled, xm))
-        return st::int4_mm_f16(ctx, p.x, xm == XM_F32, p.perm, p.qw, p.sc, p.qz, p.zoff, p.y, p.M, p.K, p.N, p.gs,
-                               nsrc);
+    if (use_i4mm(ctx, p, tiled, xm)) {
+        const int rc = st::int4_mm_f16(ctx, p.x, xm == XM_F32, p.perm, p.qw, p.sc, p.qz, p.zoff, p.y, p.M, p.K, p.N,
+                                       p.gs, nsrc);
+        if (rc != -1) return rc;  // (-1: the K split's partials do not fit the workspace)
+    }
     p.units = p.K / p.gs;
     p.ntiles = (p.N + kTileN - 1) / kTileN;
     // the tiled kernels address the weights with 32-bit buffer offsets

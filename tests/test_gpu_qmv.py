@@ -981,12 +981,14 @@ def test_int4_mm_f16_act_order(gpu, orc, Mr, K, N, gs, zeros, f16, dual, tune):
     (9, 4112, False, True),     # 257 tiles, 9 tokens: the f16-MFMA kernel
     (11, 4112, True, True),     # gate/up at 11 tokens
     (8, 4112, False, False),    # 8 tokens: the limb kernels
-    (10, 4096, False, False),   # 256 tiles, not more than the CUs: the limb kernels
+    (10, 4096, False, True),    # 256 tiles, not more than the CUs: groups of 8 tiles, K split across workgroups
+    (8, 4096, False, False),    # 8 tokens on 256 tiles: the limb kernels
 ])
 def test_int4_mm_f16_default_routing(gpu, orc, Mr, N, dual, want, tune):
     """Which kernel the GPTQ entry points pick by default on an MI355X (256
-    CUs): the f16-MFMA kernel from 9 tokens on linears with more 16-column
-    tiles than CUs, the integer-limb kernels otherwise. The default call's y
+    CUs): the f16-MFMA kernel from 9 tokens (with K split across workgroups
+    when there are no more 16-column tiles than CUs), the integer-limb
+    kernels below. The default call's y
     must equal, bit for bit, the call with that kernel forced; both are
     checked against the f64 oracle."""
     ncu = torch.cuda.get_device_properties(gpu.device).multi_processor_count
@@ -1012,6 +1014,50 @@ def test_int4_mm_f16_default_routing(gpu, orc, Mr, N, dual, want, tune):
     y_forced = run()
     assert orc.rel_l2(y, ref) < TOL
     np.testing.assert_array_equal(y, y_forced)
+
+
+@pytest.mark.parametrize("Mr,K,N,gs,zeros,f16,dual,act", [
+    (16, 4096, 2560, 128, False, False, False, False),  # configs[4] o: 160 tiles, 20 groups of 8, 12 K slices
+    (16, 9728, 2560, 128, False, False, False, False),  # configs[4] down: 76 units
+    (9, 11008, 4096, 128, True, False, False, False),   # Llama-7B down at 9 tokens, zeros
+    (12, 4096, 4096, 128, False, True, False, False),   # f16 x, 256 tiles
+    (10, 2048, 520, 64, True, False, False, False),     # group 64, ragged last tile
+    (13, 3072, 776, 256, False, False, False, False),   # group 256
+    (16, 2560, 1024, 128, False, False, True, False),   # gate/up on 64 tile pairs
+    (11, 1536, 776, 128, True, True, True, False),      # gate/up, f16 x, zeros
+    (16, 4096, 2560, 128, True, False, False, True),    # act-order, f32 x: pre-pass rows, then the partials
+    (14, 2048, 1040, 128, False, True, True, True),     # act-order, f16 x gathered, gate/up
+])
+def test_int4_mm_f16_k_split(gpu, orc, Mr, K, N, gs, zeros, f16, dual, act, tune):
+    """9-16 tokens on no more 16-column tiles than CUs: the f16-MFMA kernel
+    takes groups of 8 tiles with K split across workgroups (whole chunks per
+    slice), f32 partial sums in the workspace (after the pre-pass rows when
+    there are any) added in slice order by a reduce launch. Against the f64
+    oracle (1e-5), against the integer-limb kernels, and deterministic."""
+    xd = np.float16 if f16 else np.float32
+    c = orc.gptq_case(400 + Mr, K, N, gs, zeros=zeros, act_order=act, M=Mr, x_dtype=xd)
+    w = up(gpu, c)
+    dt = torch.float16 if f16 else torch.float32
+    f64 = lambda cc: orc.gptq_matvec_f64(c["x"], cc["qweight"], cc["scales"], K, N, gs, qzeros=cc["qzeros"],
+                                         g_idx=c["g_idx"] if act else None)
+    ref = f64(c)
+    if dual:
+        c2 = orc.gptq_case(410 + Mr, K, N, gs, zeros=zeros)
+        if act:
+            c2["g_idx"] = c["g_idx"]
+        w2 = up(gpu, c2)
+        ref = orc.silu_gate_f64(ref, f64(c2))
+        run = lambda: _gate_up(gpu, w, w2, c["x"], dt)
+    else:
+        run = lambda: run_matvec(gpu, w, c["x"], dt)
+    tune(I4MM_MIN_M=2)
+    y = run()
+    e = orc.rel_l2(y, ref)
+    print(f"int4 f16-MFMA K split M={Mr} K={K} N={N} gs={gs} dual={dual} act={act} rel-L2 {e:.3e}")
+    assert np.isfinite(y).all() and e < 1e-5
+    np.testing.assert_array_equal(run(), y)
+    tune(I4MM_SPLIT_TILES=0)
+    assert orc.rel_l2(run(), ref) < TOL
 
 
 def test_int4_mm_f16_integer_exact(gpu, orc, tune):
