@@ -105,7 +105,7 @@ typedef enum {
     ST_TUNE_NO_KSPLIT,         /* 1: no split-K of several-token decode on few tiles */
     ST_TUNE_SPLIT_TILES_CU,    /* several-token decode: split K up to this many tiles per CU */
     ST_TUNE_TOKEN_BLOCK,       /* decode: tokens per launch (1..16) */
-    ST_TUNE_I4MM_MIN_M,        /* GPTQ decode: fewest tokens for the f16-MFMA kernel */
+    ST_TUNE_I4MM_MIN_M,        /* GPTQ decode: fewest tokens for the f16-MFMA kernel (default 5 on more tiles than CUs, 9 on fewer) */
     ST_TUNE_I4MM_MIN_TILES,    /* GPTQ decode: fewest 16-column tiles for the f16-MFMA kernel */
     ST_TUNE_I8MM_MIN_M,        /* INT8 decode: fewest tokens for the f16-MFMA kernel */
     ST_TUNE_GEMM_CB,           /* prefill GEMM: 32-column blocks per wave (1 or 2) */

@@ -67,20 +67,26 @@ __global__ __launch_bounds__(256) void repack8_kernel(const int8_t *__restrict__
 }
 
 // The GPTQ entry points take the f16-MFMA kernel (tiled weights, with or
-// without act-order, f32 or f16 x) from this many tokens on, when N has more
-// 16-column tiles than the GPU has CUs (as measured on configs[4]'s shapes:
-// at 16 tokens q|k|v 12.0 -> 10.7 us, gate/up 20.2 -> 17.4, lm_head 134 -> 75;
-// from 9 tokens on (three 4-token blocks for the limb kernels) Llama-7B gate/up
-// 26.5 -> 23.2 us, configs[4] q|k|v 11.5 -> 10.4 and gate/up 18.1 -> 16.2;
-// with fewer tiles, or at 2-8 tokens, the integer-limb kernels are faster).
-constexpr int kI4mmMinM = 9;
+// without act-order, f32 or f16 x) from kI4mmMinM tokens on when N has more
+// 16-column tiles than the GPU has CUs, and from kI4mmSplitMinM tokens on
+// (groups of tiles, K split across workgroups) when it has fewer. Measured
+// against the integer-limb kernels (kernel durations, MI355X): at 5 tokens
+// configs[4] q|k|v 9.45 -> 7.61 us, gate/up 12.44 -> 9.58, the lm_head
+// 77.3 -> 51.3, Llama-7B gate/up 14.95 -> 11.86; at 4 tokens the lm_head
+// stays on the streaming kernel (39.3 against 50.9 us). On few tiles the
+// limb kernels' fused split-K reduction keeps 5-8 tokens (configs[4] o at 8
+// tokens 9.24 against 10.27 us); at 9-16 tokens the split kernel wins
+// (o 11.8 -> 10.5, down 16.4 -> 12.3, Llama-7B down 21.8 -> 13.7 us).
+constexpr int kI4mmMinM = 5;
+constexpr int kI4mmSplitMinM = 9;
 
 bool use_i4mm(const st_context *ctx, const QmvParams &p, bool tiled, int xm) {
     const int ntiles = (p.N + kTileN - 1) / kTileN;
-    const int min_m = std::max(2, st::tune(ctx, ST_TUNE_I4MM_MIN_M, kI4mmMinM));
+    const bool few = ntiles <= ctx->num_cus;
+    const int min_m = std::max(2, st::tune(ctx, ST_TUNE_I4MM_MIN_M, few ? kI4mmSplitMinM : kI4mmMinM));
     const int min_tiles = st::tune(ctx, ST_TUNE_I4MM_MIN_TILES, ctx->num_cus + 1);
-    const bool few = ntiles <= ctx->num_cus && st::tune(ctx, ST_TUNE_I4MM_SPLIT_TILES, st::kI4mmSplitTiles) > 0;
-    return tiled && (xm == XM_F32 || xm == XM_F16) && p.M <= 16 && p.M >= min_m && (ntiles >= min_tiles || few) &&
+    const bool split = few && st::tune(ctx, ST_TUNE_I4MM_SPLIT_TILES, st::kI4mmSplitTiles) > 0;
+    return tiled && (xm == XM_F32 || xm == XM_F16) && p.M <= 16 && p.M >= min_m && (ntiles >= min_tiles || split) &&
            p.K % 128 == 0 && (size_t)ntiles * kTileN * p.K / 2 < (size_t(1) << 31);
 }
 

@@ -978,17 +978,18 @@ def test_int4_mm_f16_act_order(gpu, orc, Mr, K, N, gs, zeros, f16, dual, tune):
 
 
 @pytest.mark.parametrize("Mr,N,dual,want", [
-    (9, 4112, False, True),     # 257 tiles, 9 tokens: the f16-MFMA kernel
+    (5, 4112, False, True),     # 257 tiles, 5 tokens: the f16-MFMA kernel
     (11, 4112, True, True),     # gate/up at 11 tokens
-    (8, 4112, False, False),    # 8 tokens: the limb kernels
+    (6, 4112, True, True),      # gate/up at 6 tokens
+    (4, 4112, False, False),    # 4 tokens: the limb (or streaming) kernels
     (10, 4096, False, True),    # 256 tiles, not more than the CUs: groups of 8 tiles, K split across workgroups
     (8, 4096, False, False),    # 8 tokens on 256 tiles: the limb kernels
 ])
 def test_int4_mm_f16_default_routing(gpu, orc, Mr, N, dual, want, tune):
     """Which kernel the GPTQ entry points pick by default on an MI355X (256
-    CUs): the f16-MFMA kernel from 9 tokens (with K split across workgroups
-    when there are no more 16-column tiles than CUs), the integer-limb
-    kernels below. The default call's y
+    CUs): the f16-MFMA kernel from 5 tokens on linears with more 16-column
+    tiles than CUs and from 9 tokens on the others (with K split across
+    workgroups), the integer-limb kernels below. The default call's y
     must equal, bit for bit, the call with that kernel forced; both are
     checked against the f64 oracle."""
     ncu = torch.cuda.get_device_properties(gpu.device).multi_processor_count
