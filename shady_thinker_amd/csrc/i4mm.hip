@@ -24,6 +24,9 @@
 //    LDS (double buffered, one chunk ahead); each wave keeps a ring of three
 //    chunks of weights, scales and zeros, two in flight while it computes
 //    one. Partial sums meet in LDS in a fixed order.
+//  * On at most one tile per CU (narrow linears): groups of tiles with K
+//    split across workgroups, whole chunks per slice; each slice's sums go
+//    to the workspace and i4mm_reduce_kernel adds them in slice order.
 #include "common.hpp"
 
 #include <algorithm>
