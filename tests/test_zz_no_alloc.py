@@ -25,11 +25,13 @@ def _mv(gpu, fn, x, w, y):
 
 
 @pytest.mark.parametrize("first,second", [
-    # (tokens, K, N, zeros): 16 tokens on 384 tiles take the f16-MFMA kernel,
-    # whose f32-x split lives in the scratch; 5 tokens on 160 tiles split K
-    # across workgroups, partial sums in the scratch
+    # (tokens, K, N, zeros): 16 tokens on 384 tiles take the f16-MFMA kernel;
+    # 5 tokens on 160 tiles take the limb kernels with K split across
+    # workgroups, partial sums in the scratch; 9-16 tokens on 64-160 tiles
+    # the f16-MFMA kernel with K split, its partials in the scratch
     ((16, 2560, 6144, False), (5, 4096, 2560, True)),
     ((12, 2560, 6144, True), (3, 9728, 2560, False)),
+    ((16, 9728, 2560, False), (9, 4096, 1024, True)),
 ])
 def test_noalloc_matches_matvec(gpu, orc, first, second):
     for seed, (Mr, K, N, zeros) in enumerate((first, second)):
