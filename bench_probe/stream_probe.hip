@@ -4,7 +4,7 @@
 // each decode kernel's algorithmic byte count, with the same graph replay and
 // cold-cache rotation as the kernels, so each kernel's time can be set beside
 // the fastest a launch of that size can read its bytes on the same box.
-// Not part of the product path (a separate library, libshady_probe.so, loaded
+// Not part of the product path (a separate library, libstream_probe.so, loaded
 // only by the benchmark); it has no reference counterpart.
 #include <hip/hip_ext.h>
 #include <hip/hip_runtime.h>
