@@ -1258,16 +1258,21 @@ namespace qmv {
 //  * one source with 2-4 tokens from 2 tiles per CU on, with 8-wave
 //    workgroups (4096 x 11008: 9.0 / 11.5 / 14.6-15.1 -> 8.7 / 8.8 / 10.0 us
 //    at 2 / 3 / 4 tokens);
-//  * one GPTQ source with one token from 2.5 tiles per CU on, with 8-wave
-//    workgroups (4096 x 11008, 2.7 tiles per CU: 8.3-8.4 -> 7.8-7.9 us;
-//    4096 x 14336: 9.7-9.9 -> 9.2-9.5 us; 2560 x 9728, 2.4 tiles per CU, is a
-//    tie). INT8 with one token keeps the register-ring kernel below 8 tiles
-//    per CU (configs[2], 3.4 tiles per CU: 16.2 against 16.4-16.5 us).
+//  * one GPTQ source with one token from 2.5 tiles per CU on when K >=
+//    kStreamLongK, with 8-wave workgroups (4096 x 12288, 3 tiles per CU:
+//    7.5 -> 7.25 us; 4096 x 16384: 9.3 -> 8.6 us; 4096 x 10240, 2.5 tiles
+//    per CU, within noise), and with a shorter K only above 4 tiles per CU,
+//    where the register-ring kernel's workgroups run out of tiles (2560 x
+//    10240, configs[4]'s gated q|k|v: 6.08 against 6.40 us on the ring;
+//    2560 x 16384 6.81 against 6.89; 2560 x 20480 10.7 against 7.8). INT8
+//    with one token keeps the register-ring kernel below 8 tiles per CU
+//    (configs[2], 3.4 tiles per CU: 16.2 against 16.4-16.5 us).
 // With fewer tiles the register-ring kernel is 0.2-1 us faster (q_proj
 // 4.7 against 5.6, down 7.9 against 8.8, configs[4] o 4.4 against 5.6 and
 // q|k|v, 1.5 tiles per CU, 5.9-6.3 against 6.0-6.5).
 constexpr int kStreamMinTilesCu = 8;
 constexpr int kStreamMinTilesCu2 = 2;  // two sources; one source with 2+ tokens
+constexpr int kStreamLongK = 4096;     // one GPTQ source, one token: from 2.5 tiles per CU at this K
 
 // The streaming kernel when it is chosen and the call fits it, else the
 // register-ring kernels.
@@ -1278,7 +1283,8 @@ int launch_fmt(st_context *ctx, Params &p) {
         const int pick = tune(ctx, ST_TUNE_DECODE_KERNEL, -1);
         const int tiles_cu = (p.ntiles + ncu - 1) / ncu;
         const bool many = NSRC == 1 && tiles_cu >= kStreamMinTilesCu;  // 16-wave workgroups
-        const bool gptq_mid = !is_i8(FMT) && 2 * p.ntiles >= 5 * ncu;  // one GPTQ source, 2.5+ tiles per CU
+        // one GPTQ source: 2.5+ tiles per CU with a long K, else 4+
+        const bool gptq_mid = !is_i8(FMT) && 2 * p.ntiles >= 5 * ncu && (p.K >= kStreamLongK || p.ntiles > 4 * ncu);
         const bool auto_stream = NSRC == 2 ? tiles_cu >= kStreamMinTilesCu2
                                            : (many || gptq_mid || (p.M >= 2 && p.ntiles >= kStreamMinTilesCu2 * ncu));
         const int waves = many ? 16 : 8;
