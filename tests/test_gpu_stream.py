@@ -282,3 +282,25 @@ def test_multi_token_routing(gpu, orc, Mr):
     e8 = orc.rel_l2(y8.cpu().numpy(), orc.int8_matvec_f64(c8["x"], c8["w"], c8["scale"], K8, N8))
     print(f"multi-token routing M={Mr}: GPTQ rel-L2 {e:.3e}, INT8 {e8:.3e}")
     assert e < TOL and e8 < TOL
+
+
+@pytest.mark.parametrize("K,N,kernel", [
+    (2560, 10240, RING),    # configs[4] gated q|k|v: 2.5 tiles per CU, short K: register-ring kernel
+    (2560, 20480, STREAM),  # 5 tiles per CU: more than a register-ring workgroup owns
+    (4096, 12288, STREAM),  # 3 tiles per CU, K = 4096
+])
+def test_one_token_routing(gpu, orc, K, N, kernel, tune):
+    """One token, one GPTQ source on 2.5+ tiles per CU (on an MI355X, 256
+    CUs): the streaming kernel with K >= 4096, or above 4 tiles per CU; the
+    register-ring kernel otherwise. The default call equals the forced
+    kernel bit for bit; both within the bar of the f64 oracle."""
+    ncu = torch.cuda.get_device_properties(gpu.device).multi_processor_count
+    if ncu != 256:
+        pytest.skip(f"routing thresholds are stated for 256 CUs, this GPU has {ncu}")
+    c = orc.gptq_case(380, K, N, 128, zeros=True, M=1)
+    w = up(gpu, c)
+    y = run(gpu, "f32", w, None, c["x"])
+    tune(DECODE_KERNEL=kernel)
+    assert np.array_equal(y, run(gpu, "f32", w, None, c["x"]))
+    ref = orc.gptq_matvec_f64(c["x"], c["qweight"], c["scales"], K, N, 128, qzeros=c["qzeros"])
+    assert orc.rel_l2(y, ref) < TOL
