@@ -31,8 +31,8 @@
  *  - No call allocates. The context's workspace (st_context_reserve_workspace)
  *    holds the prefill GEMM's pre-processed A and split-K partials, the
  *    split-K partials of multi-token (M > 1) decode calls on linears with few
- *    16-column tiles, and the split f32 x of 9-16-token GPTQ calls on wide
- *    linears; one-token decode calls use none. Calls on one context
+ *    16-column tiles, and the split f32 x of multi-token GPTQ calls with
+ *    act-order; one-token decode calls use none. Calls on one context
  *    are ordered by its stream, so they never overlap on it.
  */
 #ifndef SHADY_HIP_H
@@ -177,12 +177,14 @@ int st_flush(st_context *ctx);
  * Requires K % group_size == 0, group_size in {64, 128, 256}, N % 8 == 0,
  * 1 <= M <= 32, 16-byte aligned qweight and x. Accumulation: exact integer
  * products of the nibbles with a 3 x 8-bit split of x scaled by a power of
- * two per group, f32 across groups (rel-L2 vs f64 ~1e-7). For 9-16 tokens
- * (per 16-token block) on tiled weights, with or without perm, when N has more
- * 16-column tiles than the GPU has CUs: f16 MFMA on exact (q - z) and x (f16
- * x as is; f32 x split once into two f16 parts per 128 k, by a pre-pass that
- * uses the context workspace), f32 sums, rel-L2 vs f64 ~1e-7. The same rule
- * applies to st_gptq_i4_gate_up_silu. */
+ * two per group, f32 across groups (rel-L2 vs f64 ~1e-7). For 5-32 tokens
+ * on tiled weights when N has more 16-column tiles than the GPU has CUs, and
+ * 9-32 when it has fewer (then with K split across workgroups and partial
+ * sums in the context workspace), with or without perm: f16 MFMA on exact
+ * (q - z) and x (f16 x as is; f32 x split into two f16 parts per 128 k while
+ * it is staged, or with perm by a pre-pass into the context workspace), f32
+ * sums, rel-L2 vs f64 ~1e-7, the weights read once for up to 32 tokens. The
+ * same rule, up to 16 tokens, applies to st_gptq_i4_gate_up_silu. */
 int st_gptq_i4_matvec(st_context *ctx, const void *x, int x_dtype,
                       const uint32_t *qweight, const uint16_t *scales,
                       const uint32_t *qzeros, const int32_t *perm, float *y,
@@ -198,8 +200,8 @@ int st_gptq_i4_matvec(st_context *ctx, const void *x, int x_dtype,
  * context workspace. Allocates nothing. A call whose scratch would exceed
  * the array fails with ST_ERR_WORKSPACE and launches nothing. The check is
  * conservative: for f32 x (and for f16 x under act-order) it counts the
- * f16-MFMA kernel's split rows of one 16-token block, 4 M K + M K / 32 bytes
- * (f16 x with perm: 2 M K), with M capped at 16, whichever kernel the call
+ * f16-MFMA kernel's split rows of one launch, 4 M K + M K / 32 bytes
+ * (f16 x with perm: 2 M K), with M capped at 32, whichever kernel the call
  * then takes; split-K partials are not counted (they shrink or go unsplit
  * to fit the array). Every call on
  * one GPU shares that GPU's array (nothing in it needs to start at zero;

@@ -195,6 +195,8 @@ __global__ __launch_bounds__(64 * NW) void i4mm_kernel(const void *__restrict__ 
     constexpr int R = F32X ? 2 : 1;       // MFMA rows per token
     constexpr int ROWS = 16 * MB;
     constexpr int TPB = 16 / R;           // tokens per 16-row block
+    // f32 x: 2^e factors per (unit, token) of a chunk, PT tokens per unit
+    constexpr int PT = ROWS / 2 > 16 ? ROWS / 2 : 16;
     constexpr int NG = Unit<GS>::NG;
     constexpr int EK = GS == 64 ? 2 : 4;  // MFMA steps (32 k) per scaled block
     // x items of 8 k: rows (tokens, or hi/lo rows of f32 tokens) x kKC / 8
@@ -214,8 +216,8 @@ __global__ __launch_bounds__(64 * NW) void i4mm_kernel(const void *__restrict__ 
     constexpr int kXsHalves = 2 * ROWS * kPitch > kRedBytes / 2 ? 2 * ROWS * kPitch : kRedBytes / 2;
     __shared__ __align__(16) _Float16 xs[kXsHalves];
     _Float16 *const xs0 = xs, *const xs1 = xs + ROWS * kPitch;
-    __shared__ float ps0[F32X ? KCU * 16 : 1];  // 2^e per (unit, token) of the chunk in xs0 / xs1
-    __shared__ float ps1[F32X ? KCU * 16 : 1];
+    __shared__ float ps0[F32X ? KCU * PT : 1];  // 2^e per (unit, token) of the chunk in xs0 / xs1
+    __shared__ float ps1[F32X ? KCU * PT : 1];
 
     // The wave index through readfirstlane: the compiler takes tid >> 6 as
     // divergent, and the source chosen from it (gate or up) then put the
@@ -288,8 +290,8 @@ __global__ __launch_bounds__(64 * NW) void i4mm_kernel(const void *__restrict__ 
             xr[j] = __builtin_amdgcn_raw_buffer_load_b128(rx, ok ? (unsigned)(row * K + k) * 2u : kNoLoad, 0, 0);
         }
         if constexpr (F32X) {
-            const int t = tid & 15, u = c * KCU + (tid >> 4);
-            const bool ok = tid < KCU * 16 && t < M && u < uend;
+            const int t = tid % PT, u = c * KCU + tid / PT;
+            const bool ok = tid < KCU * PT && t < M && u < uend;
             pr = __builtin_amdgcn_raw_buffer_load_b32(rp, ok ? (unsigned)(t * units + u) * 4u : kNoLoad, 0, 0);
         }
     };
@@ -319,7 +321,7 @@ __global__ __launch_bounds__(64 * NW) void i4mm_kernel(const void *__restrict__ 
                     const int t = i / (kKC / 8), kq = i % (kKC / 8);
                     *reinterpret_cast<u32x4 *>(&xs[(2 * t) * kPitch + 8 * kq]) = H;
                     *reinterpret_cast<u32x4 *>(&xs[(2 * t + 1) * kPitch + 8 * kq]) = L;
-                    if ((kq & 15) == 0) ps[(kq >> 4) * 16 + t] = __builtin_amdgcn_ldexpf(1.0f, ex);
+                    if ((kq & 15) == 0) ps[(kq >> 4) * PT + t] = __builtin_amdgcn_ldexpf(1.0f, ex);
                 }
             }
             return;
@@ -332,7 +334,7 @@ __global__ __launch_bounds__(64 * NW) void i4mm_kernel(const void *__restrict__ 
                     F32X ? xr[j] : to_b_order(xr[j]);
         }
         if constexpr (F32X) {
-            if (tid < KCU * 16) ps[tid] = __builtin_bit_cast(float, pr);
+            if (tid < KCU * PT) ps[tid] = __builtin_bit_cast(float, pr);
         }
     };
 
@@ -409,7 +411,7 @@ __global__ __launch_bounds__(64 * NW) void i4mm_kernel(const void *__restrict__ 
             f32x2 pw[MB];                     // 2^e of this lane's two tokens per block
             if constexpr (F32X) {
 #pragma unroll
-                for (int mb = 0; mb < MB; ++mb) pw[mb] = *reinterpret_cast<const f32x2 *>(&pf[ul * 16 + TPB * mb + 2 * q]);
+                for (int mb = 0; mb < MB; ++mb) pw[mb] = *reinterpret_cast<const f32x2 *>(&pf[ul * PT + TPB * mb + 2 * q]);
             }
 #pragma unroll
             for (int blk = 0; blk < 4 / EK; ++blk) {  // scaled blocks of EK steps
@@ -527,8 +529,10 @@ __global__ __launch_bounds__(64 * NW) void i4mm_kernel(const void *__restrict__ 
             if (ks > 1) {  // the slice's sums, to i4mm_reduce_kernel
 #pragma unroll
                 for (int sr = 0; sr < NSRC; ++sr) part[((size_t)(kslice * NSRC + sr) * M + m) * N + nc] = v[sr];
+            } else if constexpr (NSRC == 2) {
+                y[(size_t)m * N + nc] = silu_f(v[0]) * v[1];
             } else {
-                y[(size_t)m * N + nc] = NSRC == 2 ? silu_f(v[0]) * v[1] : v[0];
+                y[(size_t)m * N + nc] = v[0];
             }
         }
 }
@@ -572,6 +576,15 @@ int launch_gs(st_context *ctx, const void *x, const float *pe, const uint32_t *c
                        x, pe, qw[0], sc[0], qz[0], qw[1], sc[1], qz[1], zoff, y, M, K, N, ntiles, part, ks);    \
     } while (0)
 #define ST_I4MM(KCU_, GW_, NW_) ST_I4MM_P(KCU_, GW_, NW_, false)
+    // 17-32 tokens of f32 x (64 MFMA rows): 2-unit chunks (the two x buffers
+    // of 4-unit chunks would not fit the LDS)
+    if constexpr (MB == 4) {
+        if (nw == 12)
+            ST_I4MM(2, 1, 12);
+        else
+            ST_I4MM(2, 1, 16);
+        return st::launch_check("i4mm_kernel");
+    } else {
     // gate/up with both sources in a wave: wpt is then waves per tile pair
     if constexpr (NSRC == 2 && GS != 64) {  // (group 64 with two sources per wave spills)
         if (pair) {
@@ -603,9 +616,10 @@ int launch_gs(st_context *ctx, const void *x, const float *pe, const uint32_t *c
         else
             ST_I4MM(2, 1, 16);
     }
+    return st::launch_check("i4mm_kernel");
+    }
 #undef ST_I4MM
 #undef ST_I4MM_P
-    return st::launch_check("i4mm_kernel");
 }
 
 // Act-order with f16 x: xg[t, k] = x[t, perm[k]] (the sorted weight rows'
@@ -627,8 +641,12 @@ int launch_mb(st_context *ctx, const void *x, const float *pe, const uint32_t *c
               const uint32_t *const *qz, int zoff, float *y, int M, int K, int N, int gs, int ntiles, int G, int wpt,
               int nw, bool pair, float *part, int ks) {
     switch (gs) {
-        case 64:
-            return launch_gs<XM, NSRC, MB, 64>(ctx, x, pe, qw, sc, qz, zoff, y, M, K, N, ntiles, G, wpt, nw, pair, part, ks);
+        case 64:  // (four 16-row blocks with group 64 spill: the entry point takes 16-token blocks)
+            if constexpr (MB == 4)
+                return st::fail(ST_ERR_UNSUPPORTED, "int4_mm_f16: group 64 with %d tokens of f32 x", M);
+            else
+                return launch_gs<XM, NSRC, MB, 64>(ctx, x, pe, qw, sc, qz, zoff, y, M, K, N, ntiles, G, wpt, nw, pair, part,
+                                                   ks);
         case 128:
             return launch_gs<XM, NSRC, MB, 128>(ctx, x, pe, qw, sc, qz, zoff, y, M, K, N, ntiles, G, wpt, nw, pair, part, ks);
         default:
@@ -640,10 +658,18 @@ template <int XM, int NSRC>
 int launch_src(st_context *ctx, const void *x, const float *pe, const uint32_t *const *qw, const uint16_t *const *sc,
                const uint32_t *const *qz, int zoff, float *y, int M, int K, int N, int gs, int ntiles, int G, int wpt,
                int nw, bool pair, float *part, int ks) {
-    // tokens per 16-row block: 8 (f32 x: hi and lo rows) or 16
+    // tokens per 16-row block: 8 (f32 x: hi and lo rows) or 16; four blocks
+    // only for one source with f32 x (17-32 tokens)
     const int mb = (M * (XM ? 2 : 1) + 15) / 16;
-    int rc = mb <= 1 ? launch_mb<XM, NSRC, 1>(ctx, x, pe, qw, sc, qz, zoff, y, M, K, N, gs, ntiles, G, wpt, nw, pair, part, ks)
-                     : launch_mb<XM, NSRC, 2>(ctx, x, pe, qw, sc, qz, zoff, y, M, K, N, gs, ntiles, G, wpt, nw, pair, part, ks);
+    int rc;
+    if (mb <= 1)
+        rc = launch_mb<XM, NSRC, 1>(ctx, x, pe, qw, sc, qz, zoff, y, M, K, N, gs, ntiles, G, wpt, nw, pair, part, ks);
+    else if (mb <= 2)
+        rc = launch_mb<XM, NSRC, 2>(ctx, x, pe, qw, sc, qz, zoff, y, M, K, N, gs, ntiles, G, wpt, nw, pair, part, ks);
+    else if constexpr (XM != 0 && NSRC == 1)
+        rc = launch_mb<XM, NSRC, 4>(ctx, x, pe, qw, sc, qz, zoff, y, M, K, N, gs, ntiles, G, wpt, nw, pair, part, ks);
+    else
+        return st::fail(ST_ERR_SHAPE, "int4_mm_f16: %d tokens", M);
     if (rc || ks == 1) return rc;
     const int mn = M * N;
     st::launch(ctx, (i4mm_reduce_kernel<NSRC>), dim3((mn + 255) / 256), dim3(256), 0, part, y, mn, ks);
@@ -675,6 +701,7 @@ int int4_mm_f16(st_context *ctx, const void *x, bool x_f32, const int32_t *perm,
     const int tbmax = (ntiles + G - 1) / G;
     int wpt = 2;  // waves per tile and source: a power of two, wpt * nsrc * tbmax <= 16
     while (wpt < 8 && 2 * wpt * nsrc * tbmax <= kWaves) wpt *= 2;
+    if (x_f32 && M > 16) wpt = 2;  // 17-32 tokens of f32 x: 2-unit chunks only
     if (wpt * nsrc * tbmax > kWaves) return fail(ST_ERR_SHAPE, "int4_mm_f16: %d tiles per workgroup", tbmax);
     // 12-wave workgroups when the tiles use at most 12 waves (gate/up with 3
     // tile pairs per workgroup): idle waves would still issue the loop's VALU

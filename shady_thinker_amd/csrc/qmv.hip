@@ -80,13 +80,15 @@ __global__ __launch_bounds__(256) void repack8_kernel(const int8_t *__restrict__
 constexpr int kI4mmMinM = 5;
 constexpr int kI4mmSplitMinM = 9;
 
-bool use_i4mm(const st_context *ctx, const QmvParams &p, bool tiled, int xm) {
+// mmax: 16, or 32 for one source (17-32 tokens in one launch, the weights
+// read once; the integer-limb kernels take 16-token blocks)
+bool use_i4mm(const st_context *ctx, const QmvParams &p, bool tiled, int xm, int mmax = 16) {
     const int ntiles = (p.N + kTileN - 1) / kTileN;
     const bool few = ntiles <= ctx->num_cus;
     const int min_m = std::max(2, st::tune(ctx, ST_TUNE_I4MM_MIN_M, few ? kI4mmSplitMinM : kI4mmMinM));
     const int min_tiles = st::tune(ctx, ST_TUNE_I4MM_MIN_TILES, ctx->num_cus + 1);
     const bool split = few && st::tune(ctx, ST_TUNE_I4MM_SPLIT_TILES, st::kI4mmSplitTiles) > 0;
-    return tiled && (xm == XM_F32 || xm == XM_F16) && p.M <= 16 && p.M >= min_m && (ntiles >= min_tiles || split) &&
+    return tiled && (xm == XM_F32 || xm == XM_F16) && p.M <= mmax && p.M >= min_m && (ntiles >= min_tiles || split) &&
            p.K % 128 == 0 && (size_t)ntiles * kTileN * p.K / 2 < (size_t(1) << 31);
 }
 
@@ -169,6 +171,13 @@ int st_gptq_i4_matvec(st_context *ctx, const void *x, int x_dtype, const uint32_
     p.zoff = (flags & ST_FLAG_ZEROS_PLUS_ONE) ? 1 : 0;
     const bool tiled = flags & ST_FLAG_TILED;
     const int xm = x_dtype == ST_F32 ? XM_F32 : XM_F16;
+    // 17-32 tokens in one f16-MFMA launch when it takes the call (not group
+    // 64 with f32 x: its four 16-row blocks would spill)
+    if (M > kTokenBlock && !(group_size == 64 && xm == XM_F32) && use_i4mm(ctx, p, tiled, xm, 2 * kTokenBlock)) {
+        const int rc = st::int4_mm_f16(ctx, p.x, xm == XM_F32, p.perm, p.qw, p.sc, p.qz, p.zoff, p.y, p.M, p.K, p.N,
+                                       p.gs, 1);
+        if (rc != -1) return rc;  // (-1: the K split's partials do not fit the workspace)
+    }
     return by_token_blocks(ctx, p, xm, [&](QmvParams &q) { return launch_i4(ctx, q, tiled, 1, xm); });
 }
 
@@ -177,13 +186,13 @@ int st_gptq_i4_matvec_noalloc(st_context *ctx, const void *x, int x_dtype, const
                               int K, int N, int group_size, uint32_t flags) {
     if (!ctx) return st::fail(ST_ERR_INVALID, "st_gptq_i4_matvec_noalloc: ctx is NULL");
     if (!ctx->scratch) return st::fail(ST_ERR_WORKSPACE, "st_gptq_i4_matvec_noalloc: no scratch on this device");
-    // The most any path of the call keeps: the f16-MFMA kernel's split of one
-    // 16-token block of f32 x (2 f16 rows per token and a factor per 128 k)
+    // The most any path of the call keeps: the f16-MFMA kernel's split of up
+    // to 32 tokens of f32 x (one launch; 2 f16 rows per token and a factor per 128 k)
     // or, for f16 x under act-order, its gathered rows; split-K partials
     // shrink (or go unsplit) to fit what is there.
     if (M > 0 && K > 0 && (x_dtype == ST_F32 || perm)) {
         // (f16 x under act-order: the gathered rows, mb K halves)
-        const size_t mb = (size_t)std::min(M, kTokenBlock);
+        const size_t mb = (size_t)std::min(M, 2 * kTokenBlock);
         const size_t need = x_dtype == ST_F32 ? 2 * mb * K * 2 + mb * (size_t)(K / 128) * 4 : mb * K * 2;
         if (need > ST_NOALLOC_SCRATCH_BYTES)
             return st::fail(ST_ERR_WORKSPACE, "st_gptq_i4_matvec_noalloc: %zu bytes of scratch needed, %u held", need,

@@ -1061,6 +1061,34 @@ def test_int4_mm_f16_k_split(gpu, orc, Mr, K, N, gs, zeros, f16, dual, act, tune
     assert orc.rel_l2(run(), ref) < TOL
 
 
+@pytest.mark.parametrize("Mr,K,N,gs,zeros,f16,act", [
+    (32, 2560, 10240, 128, False, False, False),  # configs[4] q|k|v at 32 tokens: 64 MFMA rows
+    (17, 2048, 6160, 256, True, False, False),    # 17 tokens, group 256, ragged last tile
+    (24, 9728, 2560, 128, True, False, False),    # few tiles: K split across workgroups
+    (32, 1024, 8200, 128, False, True, False),    # f16 x: two 16-row blocks
+    (20, 2048, 4160, 128, True, False, True),     # act-order: the pre-pass splits 20 tokens
+    (32, 1024, 4160, 64, False, False, False),    # group 64 with f32 x: 16-token blocks
+])
+def test_int4_mm_f16_32_tokens(gpu, orc, Mr, K, N, gs, zeros, f16, act, tune):
+    """17-32 tokens in one f16-MFMA launch (the weights read once; f32 x as
+    64 hi/lo rows, 2-unit chunks), against the f64 oracle (1e-5), equal to
+    the same call in 16-token pieces on the integer-limb kernels within the
+    bar, and deterministic."""
+    xd = np.float16 if f16 else np.float32
+    c = orc.gptq_case(430 + Mr, K, N, gs, zeros=zeros, act_order=act, M=Mr, x_dtype=xd)
+    w = up(gpu, c)
+    dt = torch.float16 if f16 else torch.float32
+    ref = orc.gptq_matvec_f64(c["x"], c["qweight"], c["scales"], K, N, gs, qzeros=c["qzeros"],
+                              g_idx=c["g_idx"] if act else None)
+    y = run_matvec(gpu, w, c["x"], dt)
+    e = orc.rel_l2(y, ref)
+    print(f"int4 f16-MFMA {Mr} tokens K={K} N={N} gs={gs} act={act} rel-L2 {e:.3e}")
+    assert np.isfinite(y).all() and e < 1e-5
+    np.testing.assert_array_equal(run_matvec(gpu, w, c["x"], dt), y)
+    tune(I4MM_MIN_M=99)
+    assert orc.rel_l2(run_matvec(gpu, w, c["x"], dt), ref) < TOL
+
+
 def test_int4_mm_f16_integer_exact(gpu, orc, tune):
     """Integer x, unit scales, zeros: every product and partial sum is an
     integer below 2^24, so y equals the exact integer result bit for bit
