@@ -1,5 +1,6 @@
-// Multi-token GPTQ int4 decode on f16 MFMA (a skinny GEMM), for 2..16
-// tokens on tiled weights (st_gptq_i4_repack) without act-order:
+// Multi-token GPTQ int4 decode on f16 MFMA (a skinny GEMM), for 2..32
+// tokens (gate/up: 2..16) on tiled weights (st_gptq_i4_repack; act-order x
+// through a pre-pass):
 //   y[m, n]  = sum_g s[g, n] * sum_{k in g} (q[k, n] - z[g, n]) * x[m, k]
 //   (st_gptq_i4_matvec), or silu(gate) * up of two such sums
 //   (st_gptq_i4_gate_up_silu). Semantics of gptq_matvec.wgsl:51-58 and
@@ -585,38 +586,38 @@ int launch_gs(st_context *ctx, const void *x, const float *pe, const uint32_t *c
             ST_I4MM(2, 1, 16);
         return st::launch_check("i4mm_kernel");
     } else {
-    // gate/up with both sources in a wave: wpt is then waves per tile pair
-    if constexpr (NSRC == 2 && GS != 64) {  // (group 64 with two sources per wave spills)
-        if (pair) {
-            if (wpt >= 4)
-                ST_I4MM_P(4, 1, 12, true);
+        // gate/up with both sources in a wave: wpt is then waves per tile pair
+        if constexpr (NSRC == 2 && GS != 64) {  // (group 64 with two sources per wave spills)
+            if (pair) {
+                if (wpt >= 4)
+                    ST_I4MM_P(4, 1, 12, true);
+                else
+                    ST_I4MM_P(2, 1, 12, true);
+                return st::launch_check("i4mm_kernel");
+            }
+        }
+        // waves per tile and source = 128-k units per chunk (one unit per wave):
+        // 8 (1024-k chunks), 4 or 2. Group size 64 stops at 4: its 8-unit chunk
+        // spilled 30 VGPRs inside the loop (one source, 16 tokens, 2560 x 6144:
+        // 15.5 -> 13.7 us with 4; gate/up unchanged).
+        if constexpr (GS != 64) {
+            if (wpt >= 8) {
+                ST_I4MM(8, 1, 16);
+                return st::launch_check("i4mm_kernel");
+            }
+        }
+        if (wpt >= 4) {
+            if (nw == 12)
+                ST_I4MM(4, 1, 12);
             else
-                ST_I4MM_P(2, 1, 12, true);
-            return st::launch_check("i4mm_kernel");
+                ST_I4MM(4, 1, 16);
+        } else {
+            if (nw == 12)
+                ST_I4MM(2, 1, 12);
+            else
+                ST_I4MM(2, 1, 16);
         }
-    }
-    // waves per tile and source = 128-k units per chunk (one unit per wave):
-    // 8 (1024-k chunks), 4 or 2. Group size 64 stops at 4: its 8-unit chunk
-    // spilled 30 VGPRs inside the loop (one source, 16 tokens, 2560 x 6144:
-    // 15.5 -> 13.7 us with 4; gate/up unchanged).
-    if constexpr (GS != 64) {
-        if (wpt >= 8) {
-            ST_I4MM(8, 1, 16);
-            return st::launch_check("i4mm_kernel");
-        }
-    }
-    if (wpt >= 4) {
-        if (nw == 12)
-            ST_I4MM(4, 1, 12);
-        else
-            ST_I4MM(4, 1, 16);
-    } else {
-        if (nw == 12)
-            ST_I4MM(2, 1, 12);
-        else
-            ST_I4MM(2, 1, 16);
-    }
-    return st::launch_check("i4mm_kernel");
+        return st::launch_check("i4mm_kernel");
     }
 #undef ST_I4MM
 #undef ST_I4MM_P
