@@ -22,9 +22,9 @@ for a block of tokens:
 * `decode` (1-32 tokens, f32 activations): the input projections as one
   concatenated linear (q|k|v, or in_proj_qkv|in_proj_z), the output
   projection (o, or out_proj on silu(z) * o through st_gptq_i4_silu_matvec),
-  gate/up fused into h = silu(x.Wg) * (x.Wu), down on h; every call one decode
-  entry point (matvec kernels, or the f16-MFMA skinny kernel for 9-16 tokens
-  on wide linears).
+  gate/up fused into h = silu(x.Wg) * (x.Wu) (in 16-token calls), down on h;
+  every call one decode entry point (the matvec kernels, or the f16-MFMA
+  skinny kernel from 5 tokens on wide linears and from 9 on narrow ones).
 * `prefill` (any number of tokens, f16 activations): the same projections
   through the prefill GEMM, with the down projections on silu(a) * b fused
   into the GEMM's A pre-pass (`st_gptq_i4_silu_gemm`).
