@@ -184,7 +184,7 @@ int st_flush(st_context *ctx);
  * (q - z) and x (f16 x as is; f32 x split into two f16 parts per 128 k while
  * it is staged, or with perm by a pre-pass into the context workspace), f32
  * sums, rel-L2 vs f64 ~1e-7, the weights read once for up to 32 tokens. The
- * same rule, up to 16 tokens, applies to st_gptq_i4_gate_up_silu. */
+ * same rule applies to st_gptq_i4_gate_up_silu. */
 int st_gptq_i4_matvec(st_context *ctx, const void *x, int x_dtype,
                       const uint32_t *qweight, const uint16_t *scales,
                       const uint32_t *qzeros, const int32_t *perm, float *y,
@@ -224,7 +224,8 @@ int st_gptq_i4_silu_matvec(st_context *ctx, const float *a, const float *b,
 /* y = silu(x . dequant(Wg)) * (x . dequant(Wu)), both [K, N].
  * Replaces fused_gate_up_silu(_4t).wgsl (src/shaders/fused_gate_up_silu_4t.wgsl:28-91,
  * declared at src/model.rs:8; the reference's forward runs gate and up as two
- * gptq_matvec calls at src/model.rs:803-808). Both weights share perm. */
+ * gptq_matvec calls at src/model.rs:803-808). Both weights share perm.
+ * 1 <= M <= 32; other arguments as st_gptq_i4_matvec. */
 int st_gptq_i4_gate_up_silu(st_context *ctx, const void *x, int x_dtype,
                             const uint32_t *qweight_gate, const uint16_t *scales_gate,
                             const uint32_t *qzeros_gate, const uint32_t *qweight_up,

@@ -1,5 +1,5 @@
 // Multi-token GPTQ int4 decode on f16 MFMA (a skinny GEMM), for 2..32
-// tokens (gate/up: 2..16) on tiled weights (st_gptq_i4_repack; act-order x
+// tokens on tiled weights (st_gptq_i4_repack; act-order x
 // through a pre-pass):
 //   y[m, n]  = sum_g s[g, n] * sum_{k in g} (q[k, n] - z[g, n]) * x[m, k]
 //   (st_gptq_i4_matvec), or silu(gate) * up of two such sums
@@ -660,14 +660,14 @@ int launch_src(st_context *ctx, const void *x, const float *pe, const uint32_t *
                const uint32_t *const *qz, int zoff, float *y, int M, int K, int N, int gs, int ntiles, int G, int wpt,
                int nw, bool pair, float *part, int ks) {
     // tokens per 16-row block: 8 (f32 x: hi and lo rows) or 16; four blocks
-    // only for one source with f32 x (17-32 tokens)
+    // only with f32 x (17-32 tokens)
     const int mb = (M * (XM ? 2 : 1) + 15) / 16;
     int rc;
     if (mb <= 1)
         rc = launch_mb<XM, NSRC, 1>(ctx, x, pe, qw, sc, qz, zoff, y, M, K, N, gs, ntiles, G, wpt, nw, pair, part, ks);
     else if (mb <= 2)
         rc = launch_mb<XM, NSRC, 2>(ctx, x, pe, qw, sc, qz, zoff, y, M, K, N, gs, ntiles, G, wpt, nw, pair, part, ks);
-    else if constexpr (XM != 0 && NSRC == 1)
+    else if constexpr (XM != 0)
         rc = launch_mb<XM, NSRC, 4>(ctx, x, pe, qw, sc, qz, zoff, y, M, K, N, gs, ntiles, G, wpt, nw, pair, part, ks);
     else
         return st::fail(ST_ERR_SHAPE, "int4_mm_f16: %d tokens", M);
@@ -711,7 +711,8 @@ int int4_mm_f16(st_context *ctx, const void *x, bool x_f32, const int32_t *perm,
     // of 12 waves (wpt becomes waves per tile pair: 3 pairs of 4 waves, or
     // 5-6 pairs of 2)
     bool pair = false;
-    if (nsrc == 2 && gs != 64 && tune(ctx, ST_TUNE_I4MM_PAIR, 1) != 0 && tune(ctx, ST_TUNE_I4MM_WAVES, 0) != 16) {
+    if (nsrc == 2 && gs != 64 && !(x_f32 && M > 16) && tune(ctx, ST_TUNE_I4MM_PAIR, 1) != 0 &&
+        tune(ctx, ST_TUNE_I4MM_WAVES, 0) != 16) {  // (not four 16-row blocks: both sources' sums would spill)
         int wpp = 2;
         while (wpp < 4 && 2 * wpp * tbmax <= 12) wpp *= 2;
         if (wpp * tbmax >= 10 && wpp * tbmax <= 12) {

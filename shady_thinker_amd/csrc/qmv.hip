@@ -236,7 +236,7 @@ int st_gptq_i4_gate_up_silu(st_context *ctx, const void *x, int x_dtype, const u
                             int K, int N, int group_size, uint32_t flags) {
     if (!ctx || !x || !qweight_gate || !scales_gate || !qweight_up || !scales_up || !y)
         return st::fail(ST_ERR_INVALID, "st_gptq_i4_gate_up_silu: NULL argument");
-    if (int rc = check_i4("st_gptq_i4_gate_up_silu", M, K, N, group_size, 16)) return rc;
+    if (int rc = check_i4("st_gptq_i4_gate_up_silu", M, K, N, group_size, 32)) return rc;
     if ((qzeros_gate == nullptr) != (qzeros_up == nullptr))
         return st::fail(ST_ERR_INVALID, "st_gptq_i4_gate_up_silu: give qzeros for both or neither");
     if (!st::aligned16(qweight_gate) || !st::aligned16(qweight_up) || !st::aligned16(x) || !st::aligned16(perm) ||
@@ -261,6 +261,11 @@ int st_gptq_i4_gate_up_silu(st_context *ctx, const void *x, int x_dtype, const u
     p.zoff = (flags & ST_FLAG_ZEROS_PLUS_ONE) ? 1 : 0;
     const bool tiled = flags & ST_FLAG_TILED;
     const int xm = x_dtype == ST_F32 ? XM_F32 : XM_F16;
+    if (M > kTokenBlock && !(group_size == 64 && xm == XM_F32) && use_i4mm(ctx, p, tiled, xm, 2 * kTokenBlock)) {
+        const int rc = st::int4_mm_f16(ctx, p.x, xm == XM_F32, p.perm, p.qw, p.sc, p.qz, p.zoff, p.y, p.M, p.K, p.N,
+                                       p.gs, 2);
+        if (rc != -1) return rc;
+    }
     return by_token_blocks(ctx, p, xm, [&](QmvParams &q) { return launch_i4(ctx, q, tiled, 2, xm); });
 }
 

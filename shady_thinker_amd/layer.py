@@ -22,7 +22,7 @@ for a block of tokens:
 * `decode` (1-32 tokens, f32 activations): the input projections as one
   concatenated linear (q|k|v, or in_proj_qkv|in_proj_z), the output
   projection (o, or out_proj on silu(z) * o through st_gptq_i4_silu_matvec),
-  gate/up fused into h = silu(x.Wg) * (x.Wu) (in 16-token calls), down on h;
+  gate/up fused into h = silu(x.Wg) * (x.Wu), down on h;
   every call one decode entry point (the matvec kernels, or the f16-MFMA
   skinny kernel from 5 tokens on wide linears and from 9 on narrow ones).
 * `prefill` (any number of tokens, f16 activations): the same projections
@@ -44,7 +44,7 @@ from ._lib import call
 from .weights import GptqWeight
 
 _DECODE_MAX = 32     # tokens per decode call (st_gptq_i4_matvec)
-_GATE_UP_BLOCK = 16  # tokens per st_gptq_i4_gate_up_silu call
+_GATE_UP_BLOCK = 32  # tokens per st_gptq_i4_gate_up_silu call
 _BF16_BLOCK = 8      # tokens per st_bf16_matvec call
 
 

@@ -1061,32 +1061,44 @@ def test_int4_mm_f16_k_split(gpu, orc, Mr, K, N, gs, zeros, f16, dual, act, tune
     assert orc.rel_l2(run(), ref) < TOL
 
 
-@pytest.mark.parametrize("Mr,K,N,gs,zeros,f16,act", [
-    (32, 2560, 10240, 128, False, False, False),  # configs[4] q|k|v at 32 tokens: 64 MFMA rows
-    (17, 2048, 6160, 256, True, False, False),    # 17 tokens, group 256, ragged last tile
-    (24, 9728, 2560, 128, True, False, False),    # few tiles: K split across workgroups
-    (32, 1024, 8200, 128, False, True, False),    # f16 x: two 16-row blocks
-    (20, 2048, 4160, 128, True, False, True),     # act-order: the pre-pass splits 20 tokens
-    (32, 1024, 4160, 64, False, False, False),    # group 64 with f32 x: 16-token blocks
+@pytest.mark.parametrize("Mr,K,N,gs,zeros,f16,act,dual", [
+    (32, 2560, 10240, 128, False, False, False, False),  # configs[4] q|k|v at 32 tokens: 64 MFMA rows
+    (17, 2048, 6160, 256, True, False, False, False),    # 17 tokens, group 256, ragged last tile
+    (24, 9728, 2560, 128, True, False, False, False),    # few tiles: K split across workgroups
+    (32, 1024, 8200, 128, False, True, False, False),    # f16 x: two 16-row blocks
+    (20, 2048, 4160, 128, True, False, True, False),     # act-order: the pre-pass splits 20 tokens
+    (32, 1024, 4160, 64, False, False, False, False),    # group 64 with f32 x: 16-token blocks
+    (32, 2560, 9728, 128, False, False, False, True),    # configs[4] gate/up at 32 tokens, one source per wave
+    (19, 1024, 2064, 256, True, True, True, True),       # gate/up, f16 x, act-order, zeros
 ])
-def test_int4_mm_f16_32_tokens(gpu, orc, Mr, K, N, gs, zeros, f16, act, tune):
+def test_int4_mm_f16_32_tokens(gpu, orc, Mr, K, N, gs, zeros, f16, act, dual, tune):
     """17-32 tokens in one f16-MFMA launch (the weights read once; f32 x as
-    64 hi/lo rows, 2-unit chunks), against the f64 oracle (1e-5), equal to
-    the same call in 16-token pieces on the integer-limb kernels within the
-    bar, and deterministic."""
+    64 hi/lo rows, 2-unit chunks; gate/up with one source per wave), against
+    the f64 oracle (1e-5), equal to the same call in 16-token pieces on the
+    integer-limb kernels within the bar, and deterministic."""
     xd = np.float16 if f16 else np.float32
     c = orc.gptq_case(430 + Mr, K, N, gs, zeros=zeros, act_order=act, M=Mr, x_dtype=xd)
     w = up(gpu, c)
     dt = torch.float16 if f16 else torch.float32
-    ref = orc.gptq_matvec_f64(c["x"], c["qweight"], c["scales"], K, N, gs, qzeros=c["qzeros"],
-                              g_idx=c["g_idx"] if act else None)
-    y = run_matvec(gpu, w, c["x"], dt)
+    f64 = lambda cc: orc.gptq_matvec_f64(c["x"], cc["qweight"], cc["scales"], K, N, gs, qzeros=cc["qzeros"],
+                                         g_idx=c["g_idx"] if act else None)
+    ref = f64(c)
+    if dual:
+        c2 = orc.gptq_case(440 + Mr, K, N, gs, zeros=zeros)
+        if act:
+            c2["g_idx"] = c["g_idx"]
+        w2 = up(gpu, c2)
+        ref = orc.silu_gate_f64(ref, f64(c2))
+        run = lambda: _gate_up(gpu, w, w2, c["x"], dt)
+    else:
+        run = lambda: run_matvec(gpu, w, c["x"], dt)
+    y = run()
     e = orc.rel_l2(y, ref)
-    print(f"int4 f16-MFMA {Mr} tokens K={K} N={N} gs={gs} act={act} rel-L2 {e:.3e}")
+    print(f"int4 f16-MFMA {Mr} tokens K={K} N={N} gs={gs} act={act} dual={dual} rel-L2 {e:.3e}")
     assert np.isfinite(y).all() and e < 1e-5
-    np.testing.assert_array_equal(run_matvec(gpu, w, c["x"], dt), y)
+    np.testing.assert_array_equal(run(), y)
     tune(I4MM_MIN_M=99)
-    assert orc.rel_l2(run_matvec(gpu, w, c["x"], dt), ref) < TOL
+    assert orc.rel_l2(run(), ref) < TOL
 
 
 def test_int4_mm_f16_integer_exact(gpu, orc, tune):
