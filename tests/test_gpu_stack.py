@@ -110,7 +110,7 @@ def _oracle_chain(orc, cases, lmc, x0):
     return logits, down
 
 
-@pytest.mark.parametrize("batch", [1, 16])
+@pytest.mark.parametrize("batch", [1, 16, 32])
 def test_stack_replay_equals_eager_and_oracle(gpu, orc, stack, batch):
     st, cases, lmc = stack
     b = st.buffers(gpu, batch)
