@@ -264,7 +264,7 @@ def main():
                     help="profiling helper: 10 plain 64 MiB device copies (calibrates FETCH_SIZE / WRITE_SIZE)")
     ap.add_argument("--only", default="", help="profiling helper: launch only this kernel, eagerly "
                                                "(q|gate_up|down|gemm|gemm512|int8gemm|lm_int4), or replay one configs[4] "
-                                               "stack step per step (stack1|stack16), or its 512-token prefill (prefill512)")
+                                               "stack step per step (stack1|stack16|stack32), or its 512-token prefill (prefill512)")
     args = ap.parse_args()
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:
@@ -328,7 +328,7 @@ def main():
                                                         flags=sta._lib.ST_FLAG_TILED), args.steps, args.warmup)
         print(json.dumps({"only": args.only, "steps": args.steps, "ms_eager": round(ms, 5)}))
         return
-    if args.only in ("stack1", "stack16"):  # configs[4] stack: graph replays (per-linear kernel times in the profile)
+    if args.only in ("stack1", "stack16", "stack32"):  # configs[4] stack: graph replays (per-linear kernel times in the profile)
         out = bench_stack(torch, dev, gpu, Mdl, gen, args, batches=(int(args.only[5:]),), prefill=False)
         print(json.dumps({"only": args.only, **out}))
         return
@@ -568,7 +568,7 @@ def bench_gemm(torch, dev, gpu, Mdl, gen, kt):
     return out
 
 
-def bench_stack(torch, dev, gpu, Mdl, gen, args, batches=(1, 16), prefill=True):
+def bench_stack(torch, dev, gpu, Mdl, gen, args, batches=(1, 16, 32), prefill=True):
     """the quantized linear stack of a 36-layer decoder
     (hidden 2560, 32 q / 8 kv heads of 128, intermediate 9728, vocab 151936),
     every linear GPTQ int4 g128 (lm_head included), random-init packed
@@ -577,7 +577,8 @@ def bench_stack(torch, dev, gpu, Mdl, gen, args, batches=(1, 16), prefill=True):
     its output gate); o reads 32 * 128 = 4096. A token = one
     DecoderStack step (per layer q|k|v as one concatenated linear, o, fused
     gate/up emitting silu(g)*u, down on it; then the lm_head), captured once
-    with DecoderStack.capture and replayed; batch 1 and 16. Attention and
+    with DecoderStack.capture and replayed; batch 1 and 16 (the config), and
+    32 (every linear in one 32-token launch). Attention and
     norms are outside the path (no hooks), so activations are synthetic."""
     H, Q, QG, KV, I, V, L = 2560, 4096, 8192, 1024, 9728, 151936, 36
     TF = sta_flags_tiled()
